@@ -1,0 +1,123 @@
+/*
+ * tmoe.h — C ABI of the MI355X (gfx950) Tucker-MoE layer forward.
+ *
+ * The reference exposes this path only as a PyTorch module, not an FFI:
+ *   pure_torch_mlx/model.py:41-102  class TuckerMoE(nn.Module)
+ *     __init__(d_in, d_out, cfg)    model.py:54-66   (cfg fields: config.py:18,20-24)
+ *     forward(x) -> out             model.py:68-102
+ *   pure_torch_mlx/weights.py:74-81 _load_tucker  (parameter / checkpoint key contract)
+ * Each entry point below names the part of that interface it replaces. A
+ * ctypes binding (the reference host language is Python) is the intended caller;
+ * every signature uses plain C types and pointers, no torch or HIP types.
+ *
+ * Conventions
+ *   - All data pointers are DEVICE pointers owned by the caller, 16-byte aligned,
+ *     row-major and contiguous. Nothing here allocates device memory or
+ *     synchronises the host with the device, except tmoe_prof_read().
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream). Work is
+ *     enqueued on it in order; results are ready when the stream reaches them.
+ *   - Every call validates its arguments on the host before any HIP call and
+ *     returns 0 on success or a negative TMOE_E* code; tmoe_last_error() then
+ *     holds a message (thread-local). Validation failures never touch the GPU,
+ *     so every error path can be exercised on a machine without one.
+ *   - A plan is immutable after creation: concurrent tmoe_forward calls with one
+ *     plan on different streams are safe when their workspaces differ.
+ */
+#ifndef TMOE_H
+#define TMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMOE_ABI_VERSION 1
+
+/* error codes */
+#define TMOE_OK            0
+#define TMOE_EINVAL       -1  /* bad argument: null/misaligned pointer, bad size     */
+#define TMOE_EUNSUPPORTED -2  /* valid for the reference, not supported by a kernel */
+#define TMOE_EHIP         -3  /* a HIP runtime call failed                           */
+
+/* element types */
+#define TMOE_F32  0
+#define TMOE_BF16 1
+
+/* Layer hyper-parameters.
+ * Replaces TuckerMoE.__init__(d_in, d_out, cfg) (model.py:54-66):
+ *   E = cfg.kmoe_num_experts, k = cfg.kmoe_top_k, r1/r2/r3 = cfg.kmoe_r1/_r2/_r3,
+ *   eps = cfg.rms_norm_eps (config.py:18,20-24). dtype = the module's parameter
+ *   dtype, which the reference forward also computes in. */
+typedef struct tmoe_shape {
+  int64_t d_in, d_out;
+  int64_t E, k;
+  int64_t r1, r2, r3;
+  int32_t dtype;   /* TMOE_BF16 or TMOE_F32: activations, weights and output */
+  float   eps;
+} tmoe_shape;
+
+typedef struct tmoe_plan tmoe_plan;
+
+/* Returns TMOE_ABI_VERSION of the loaded library. */
+int tmoe_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tmoe_last_error(void);
+
+/* Validates `shape` and builds a plan (host memory only).
+ * Replaces the shape checks torch performs inside TuckerMoE.forward: a top_k
+ * larger than E raises in torch.topk (model.py:76) and gives TMOE_EINVAL here.
+ * Shapes the reference accepts but these kernels do not (see the message) give
+ * TMOE_EUNSUPPORTED. */
+int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out);
+void tmoe_plan_destroy(tmoe_plan* plan);
+
+/* Bytes of the packed-weight buffer for tmoe_pack_weights. */
+size_t tmoe_packed_bytes(const tmoe_plan* plan);
+
+/* Bytes of device workspace tmoe_forward needs for T tokens (T >= 0). */
+size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T);
+
+/* Re-lays the module parameters into the kernels' operand layouts.
+ * Replaces the parameter set of TuckerMoE (model.py:60-66, loaded by
+ * weights.py:74-81). Inputs are the parameters as the module holds them, in the
+ * plan's dtype:
+ *   router_w (E, d_in)   U_in (d_in, r3)   inner_w (r3)   U_expert (E, r1)
+ *   core (r1, r3, r2)    U_out (r2, d_out) bias (d_out)
+ * `packed` must hold tmoe_packed_bytes(plan) bytes. Stream-ordered. The packed
+ * buffer is derived state: pack again whenever a parameter changes. */
+int tmoe_pack_weights(const tmoe_plan* plan,
+                      const void* router_w, const void* U_in, const void* inner_w,
+                      const void* U_expert, const void* core, const void* U_out,
+                      const void* bias, void* packed, void* stream);
+
+/* The layer forward for T tokens: out = TuckerMoE.forward(x) (model.py:68-102).
+ *   x        (T, d_in)   plan dtype
+ *   out      (T, d_out)  plan dtype
+ *   topk_idx (T, k) int32, nullable: selected experts, descending logit,
+ *            ties to the lower index (torch.topk's indices, model.py:76)
+ *   topk_w   (T, k) f32, nullable: softmax over the k selected logits (model.py:77)
+ *   logits   (T, E) f32, nullable: router scores x @ router_w^T (model.py:75)
+ *   workspace of at least tmoe_workspace_bytes(plan, T) bytes.
+ * T == 0 is a no-op. Stream-ordered, no allocation, no host synchronisation. */
+int tmoe_forward(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
+                 void* out, int32_t* topk_idx, float* topk_w, float* logits,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Per-stage timing, no counterpart in the reference (measurement support).
+ * While enabled, every tmoe_forward records a HIP event before each of its
+ * kernels and one after the last, on the forward's stream. tmoe_prof_read waits
+ * for those events, writes the summed milliseconds per stage into ms[0..n-1]
+ * (stage order: router, in-projection, core, out-projection), the number of
+ * forwards into *calls, and clears the record. Returns the stage count. Not
+ * thread-safe; for benchmarks only. */
+int tmoe_prof_enable(int on);
+int tmoe_prof_read(double* ms, int n, int64_t* calls);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMOE_H */

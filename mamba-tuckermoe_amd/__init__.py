@@ -1,0 +1,17 @@
+"""mamba_tuckermoe_amd — the Tucker-MoE layer forward of s990093/Mamba-TuckerMoE
+(pure_torch_mlx/model.py:41-102) on AMD Instinct MI355X (gfx950).
+
+Public surface:
+  TuckerMoE(d_in, d_out, cfg)  drop-in nn.Module (module.py)
+  TuckerMoEConfig              the cfg fields the module reads (config.py)
+  WORKLOADS                    the named seeded workloads C1..C5 (config.py)
+  load_tucker                  checkpoint-key loader that refreshes packed weights
+  synth                        seeded synthetic parameters and tokens
+  _lib                         ctypes binding of the C ABI (include/tmoe.h)
+"""
+from . import _lib, config, synth
+from .config import WORKLOADS, TuckerMoEConfig, Workload
+from .module import RMSNorm, TuckerMoE, load_tucker
+
+__all__ = ["TuckerMoE", "RMSNorm", "TuckerMoEConfig", "Workload", "WORKLOADS", "load_tucker",
+           "synth", "config", "_lib"]

@@ -1,0 +1,151 @@
+"""ctypes binding of libtmoe.so, the C ABI declared in include/tmoe.h.
+
+This is the binding a user of the reference's PyTorch module path adds: the
+reference has no FFI (pure_torch_mlx/model.py is plain PyTorch), so the library
+is reached from Python through ctypes. torch is imported first so that the
+library resolves libamdhip64.so.7 to the HIP runtime torch already loaded (one
+HIP runtime per process).
+
+There is no fallback: if the library is missing, lib() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtmoe.so")
+
+ABI_VERSION = 1
+TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
+TMOE_F32, TMOE_BF16 = 0, 1
+N_STAGES = 4
+STAGE_NAMES = ("router", "in_proj", "core", "out_proj")
+
+# Every function include/tmoe.h declares.
+EXPORTED = (
+    "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
+    "tmoe_packed_bytes", "tmoe_workspace_bytes", "tmoe_pack_weights", "tmoe_forward",
+    "tmoe_prof_enable", "tmoe_prof_read",
+)
+
+
+class TmoeShape(ctypes.Structure):
+    """struct tmoe_shape."""
+    _fields_ = [
+        ("d_in", ctypes.c_int64), ("d_out", ctypes.c_int64),
+        ("E", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("r1", ctypes.c_int64), ("r2", ctypes.c_int64), ("r3", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("eps", ctypes.c_float),
+    ]
+
+
+class TmoeError(RuntimeError):
+    """A negative return code of the C ABI, with tmoe_last_error()'s message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"tmoe error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libtmoe.so once; raises if it is not built or is the wrong ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; build it with __graft_entry__.build() "
+                "(hipcc --offload-arch=gfx950). There is no fallback path.")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+        L.tmoe_abi_version.restype = ctypes.c_int
+        L.tmoe_abi_version.argtypes = []
+        L.tmoe_last_error.restype = ctypes.c_char_p
+        L.tmoe_last_error.argtypes = []
+        L.tmoe_plan_create.restype = ctypes.c_int
+        L.tmoe_plan_create.argtypes = [ctypes.POINTER(TmoeShape), ctypes.POINTER(vp)]
+        L.tmoe_plan_destroy.restype = None
+        L.tmoe_plan_destroy.argtypes = [vp]
+        L.tmoe_packed_bytes.restype = sz
+        L.tmoe_packed_bytes.argtypes = [vp]
+        L.tmoe_workspace_bytes.restype = sz
+        L.tmoe_workspace_bytes.argtypes = [vp, i64]
+        L.tmoe_pack_weights.restype = ctypes.c_int
+        L.tmoe_pack_weights.argtypes = [vp] * 10
+        L.tmoe_forward.restype = ctypes.c_int
+        L.tmoe_forward.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]
+        L.tmoe_prof_enable.restype = ctypes.c_int
+        L.tmoe_prof_enable.argtypes = [ctypes.c_int]
+        L.tmoe_prof_read.restype = ctypes.c_int
+        L.tmoe_prof_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.c_int,
+                                     ctypes.POINTER(ctypes.c_int64)]
+        v = L.tmoe_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI version {v}, expected {ABI_VERSION}")
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> int:
+    """Raises TmoeError for a negative return code."""
+    if rc < 0:
+        raise TmoeError(rc, lib().tmoe_last_error().decode(errors="replace"))
+    return rc
+
+
+class Plan:
+    """Owns a tmoe_plan*. Immutable; safe to share across streams."""
+
+    def __init__(self, d_in, d_out, E, k, r1, r2, r3, dtype: torch.dtype, eps: float):
+        if dtype == torch.bfloat16:
+            code = TMOE_BF16
+        elif dtype == torch.float32:
+            code = TMOE_F32
+        else:
+            raise TmoeError(TMOE_EUNSUPPORTED,
+                            f"parameter dtype {dtype}: supported are bfloat16 and float32")
+        self.shape = TmoeShape(d_in, d_out, E, k, r1, r2, r3, code, eps)
+        self.dtype = dtype
+        self._ptr = ctypes.c_void_p()
+        L = lib()
+        check(L.tmoe_plan_create(ctypes.byref(self.shape), ctypes.byref(self._ptr)))
+        self._destroy = L.tmoe_plan_destroy
+
+    @property
+    def ptr(self):
+        return self._ptr
+
+    def packed_bytes(self) -> int:
+        return int(lib().tmoe_packed_bytes(self._ptr))
+
+    def workspace_bytes(self, T: int) -> int:
+        return int(lib().tmoe_workspace_bytes(self._ptr, T))
+
+    def __del__(self):
+        ptr, self._ptr = getattr(self, "_ptr", None), None
+        if ptr and getattr(self, "_destroy", None):
+            self._destroy(ptr)
+
+
+def prof_enable(on: bool) -> None:
+    check(lib().tmoe_prof_enable(1 if on else 0))
+
+
+def prof_read():
+    """Returns (ms summed per stage, number of forwards) since the last read."""
+    ms = (ctypes.c_double * N_STAGES)()
+    calls = ctypes.c_int64()
+    check(lib().tmoe_prof_read(ms, N_STAGES, ctypes.byref(calls)))
+    return list(ms), int(calls.value)

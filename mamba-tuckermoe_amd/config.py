@@ -1,0 +1,85 @@
+"""Layer hyper-parameters and the named workloads C1..C5.
+
+`TuckerMoEConfig` carries the fields TuckerMoE.__init__ reads from the
+reference's Mamba3Config (pure_torch_mlx/config.py:18,20-24; defaults copied from
+there). Any object with those attributes (the reference's own Mamba3Config
+included) is accepted by mamba_tuckermoe_amd.TuckerMoE.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+
+@dataclass
+class TuckerMoEConfig:
+    rms_norm_eps: float = 1e-5        # config.py:18
+    kmoe_num_experts: int = 8         # config.py:20
+    kmoe_top_k: int = 2               # config.py:21
+    kmoe_r1: int = 32                 # config.py:22
+    kmoe_r2: int = 512                # config.py:23
+    kmoe_r3: int = 256                # config.py:24
+
+
+@dataclass(frozen=True)
+class Workload:
+    """One seeded synthetic configuration of the layer."""
+    name: str
+    T: int
+    d_in: int
+    d_out: int
+    E: int
+    k: int
+    r1: int
+    r3: int
+    r2: int
+    dtype: torch.dtype
+    seed: int
+    router_std: Optional[float] = None   # None: N(0, 1/d_in)
+    fp8: bool = False                    # U_in, core, U_out as e4m3 + per-channel scales
+    note: str = ""
+
+    def cfg(self, eps: float = 1e-5) -> TuckerMoEConfig:
+        return TuckerMoEConfig(rms_norm_eps=eps, kmoe_num_experts=self.E, kmoe_top_k=self.k,
+                               kmoe_r1=self.r1, kmoe_r2=self.r2, kmoe_r3=self.r3)
+
+    def with_T(self, T: int) -> "Workload":
+        d = dict(self.__dict__)
+        d["T"] = T
+        return Workload(**d)
+
+    def flops(self, T: Optional[int] = None) -> dict:
+        """Algorithmic MFMA work per forward: 2*T*(E*d_in + d_in*r3 + r1*r3*r2 + r2*d_out)."""
+        T = self.T if T is None else T
+        st = {
+            "router": 2 * T * self.E * self.d_in,
+            "in_proj": 2 * T * self.d_in * self.r3,
+            "core": 2 * T * self.r1 * self.r3 * self.r2,
+            "out_proj": 2 * T * self.r2 * self.d_out,
+        }
+        st["total"] = sum(st.values())
+        return st
+
+    def hbm_bytes(self, T: Optional[int] = None) -> int:
+        """Compulsory HBM bytes per forward: x in, out, every weight once."""
+        T = self.T if T is None else T
+        es = 4 if self.dtype == torch.float32 else 2
+        w = (self.E * self.d_in + self.d_in * self.r3 + self.r3 + self.E * self.r1
+             + self.r1 * self.r3 * self.r2 + self.r2 * self.d_out + self.d_out)
+        return T * self.d_in * es + T * self.d_out * es + w * es
+
+
+WORKLOADS = {
+    "C1": Workload("C1", 64, 512, 1024, 8, 2, 4, 128, 256, torch.float32, 1001,
+                   note="fp32 everywhere; the reference's CPU-path configuration"),
+    "C2": Workload("C2", 32, 1536, 2304, 16, 2, 4, 256, 1024, torch.bfloat16, 1002,
+                   note="decode-shaped: batch 32 x 1 step"),
+    "C3": Workload("C3", 16384, 1536, 2304, 16, 2, 4, 256, 1024, torch.bfloat16, 1003,
+                   note="prefill-shaped: batch 8 x seq 2048"),
+    "C4": Workload("C4", 4096, 1536, 2304, 256, 8, 4, 256, 1024, torch.bfloat16, 1004,
+                   router_std=0.02, note="expert-count scaling"),
+    "C5": Workload("C5", 16384, 1536, 2304, 16, 2, 4, 256, 1024, torch.bfloat16, 1005,
+                   fp8=True, note="fp8 e4m3 U_in/core/U_out with per-output-channel scales"),
+}

@@ -1,0 +1,295 @@
+// Host side of the C ABI declared in include/tmoe.h: argument validation, the
+// plan (packed-weight and workspace layout), and the launch sequence.
+//
+// Every entry point validates on the host before its first HIP call, so each
+// error path is reachable without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "tmoe.h"
+#include "tmoe_internal.h"
+
+struct tmoe_plan {
+  tmoe_shape s;
+  int64_t E_pad;
+  size_t es;   // element size of the plan dtype
+  // packed-weight layout (byte offsets)
+  size_t off_wr, off_uin, off_gain, off_uexp, off_core, off_uout, off_bias, packed_bytes;
+};
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(TMOE_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kStages = 4;
+
+// Per-stage event record of tmoe_prof_enable.
+struct Prof {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> free_ev;
+  std::vector<std::vector<hipEvent_t>> pending;   // kStages + 1 events per forward
+};
+Prof g_prof;
+
+hipEvent_t prof_event() {
+  if (!g_prof.free_ev.empty()) {
+    hipEvent_t e = g_prof.free_ev.back();
+    g_prof.free_ev.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+struct Layout {
+  size_t z, c, idx, w, mid, total;
+};
+
+Layout workspace_layout(const tmoe_plan* p, int64_t T) {
+  Layout L{};
+  size_t o = 0;
+  L.z = o;   o = align256(o + (size_t)T * p->s.r3 * p->es);
+  L.c = o;   o = align256(o + (size_t)T * p->s.r1 * sizeof(float));
+  L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
+  L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
+  L.mid = o; o = align256(o + (size_t)T * p->s.r2 * p->es);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmoe_abi_version(void) { return TMOE_ABI_VERSION; }
+
+const char* tmoe_last_error(void) { return g_err; }
+
+int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
+  g_err[0] = 0;
+  if (!shape || !plan_out) return fail(TMOE_EINVAL, "tmoe_plan_create: null argument");
+  *plan_out = nullptr;
+  const tmoe_shape& s = *shape;
+  if (s.dtype != TMOE_BF16 && s.dtype != TMOE_F32)
+    return fail(TMOE_EINVAL, "dtype %d is neither TMOE_BF16 nor TMOE_F32", s.dtype);
+  if (s.d_in <= 0 || s.d_out <= 0 || s.E <= 0 || s.k <= 0 || s.r1 <= 0 || s.r2 <= 0 || s.r3 <= 0)
+    return fail(TMOE_EINVAL,
+                "dimensions must be positive (d_in=%lld d_out=%lld E=%lld k=%lld r=(%lld,%lld,%lld))",
+                (long long)s.d_in, (long long)s.d_out, (long long)s.E, (long long)s.k,
+                (long long)s.r1, (long long)s.r2, (long long)s.r3);
+  if (s.k > s.E)   // torch.topk raises for k > size (model.py:76)
+    return fail(TMOE_EINVAL, "top_k=%lld exceeds the number of experts E=%lld", (long long)s.k,
+                (long long)s.E);
+  if (!(s.eps >= 0.f)) return fail(TMOE_EINVAL, "eps must be >= 0");
+  if (s.d_in % 64)
+    return fail(TMOE_EUNSUPPORTED, "d_in=%lld: must be a multiple of 64", (long long)s.d_in);
+  if (s.r3 != 64 && s.r3 != 128 && s.r3 != 256)
+    return fail(TMOE_EUNSUPPORTED, "r3=%lld: supported values are 64, 128, 256",
+                (long long)s.r3);
+  if (s.r2 % 64)
+    return fail(TMOE_EUNSUPPORTED, "r2=%lld: must be a multiple of 64", (long long)s.r2);
+  if (s.d_out % 16)
+    return fail(TMOE_EUNSUPPORTED, "d_out=%lld: must be a multiple of 16", (long long)s.d_out);
+  if (s.E > tmoe::kMaxExperts)
+    return fail(TMOE_EUNSUPPORTED, "E=%lld: at most %d experts", (long long)s.E,
+                tmoe::kMaxExperts);
+  if (s.k > tmoe::kMaxTopK)
+    return fail(TMOE_EUNSUPPORTED, "top_k=%lld: at most %d", (long long)s.k, tmoe::kMaxTopK);
+  if (s.r1 > 64)
+    return fail(TMOE_EUNSUPPORTED, "r1=%lld: at most 64", (long long)s.r1);
+
+  tmoe_plan* p = new (std::nothrow) tmoe_plan();
+  if (!p) return fail(TMOE_EINVAL, "out of host memory");
+  p->s = s;
+  p->es = s.dtype == TMOE_BF16 ? 2 : 4;
+  int64_t ep = 16;
+  while (ep < s.E) ep *= 2;   // router tile widths: 16, 32, 64, 128, 256
+  p->E_pad = ep;
+  size_t o = 0;
+  p->off_wr = o;   o = align256(o + (size_t)p->E_pad * s.d_in * p->es);
+  p->off_uin = o;  o = align256(o + (size_t)s.r3 * s.d_in * p->es);
+  p->off_gain = o; o = align256(o + (size_t)s.r3 * sizeof(float));
+  p->off_uexp = o; o = align256(o + (size_t)s.E * s.r1 * sizeof(float));
+  p->off_core = o; o = align256(o + (size_t)s.r2 * s.r1 * s.r3 * p->es);
+  p->off_uout = o; o = align256(o + (size_t)s.d_out * s.r2 * p->es);
+  p->off_bias = o; o = align256(o + (size_t)s.d_out * sizeof(float));
+  p->packed_bytes = o;
+  *plan_out = p;
+  return TMOE_OK;
+}
+
+void tmoe_plan_destroy(tmoe_plan* plan) { delete plan; }
+
+size_t tmoe_packed_bytes(const tmoe_plan* plan) { return plan ? plan->packed_bytes : 0; }
+
+size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T) {
+  if (!plan || T < 0) return 0;
+  return workspace_layout(plan, T).total;
+}
+
+int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in,
+                      const void* inner_w, const void* U_expert, const void* core,
+                      const void* U_out, const void* bias, void* packed, void* stream) {
+  g_err[0] = 0;
+  if (!p) return fail(TMOE_EINVAL, "tmoe_pack_weights: null plan");
+  const void* ptrs[] = {router_w, U_in, inner_w, U_expert, core, U_out, bias, packed};
+  const char* names[] = {"router_w", "U_in", "inner_w", "U_expert", "core", "U_out", "bias",
+                         "packed"};
+  for (int i = 0; i < 8; ++i) {
+    if (!ptrs[i]) return fail(TMOE_EINVAL, "tmoe_pack_weights: %s is null", names[i]);
+    if (i == 7 && !aligned16(ptrs[i]))
+      return fail(TMOE_EINVAL, "tmoe_pack_weights: packed is not 16-byte aligned");
+  }
+  const tmoe_shape& s = p->s;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(packed);
+  const int es = (int)p->es;
+  hipError_t e;
+  if ((e = tmoe::launch_copy_pad(router_w, base + p->off_wr, s.E * s.d_in, p->E_pad * s.d_in, es,
+                                 st)) != hipSuccess)
+    return hip_fail(e, "pack router");
+  if ((e = tmoe::launch_transpose(U_in, base + p->off_uin, s.d_in, s.r3, es, st)) != hipSuccess)
+    return hip_fail(e, "pack U_in");
+  if ((e = tmoe::launch_to_f32(inner_w, reinterpret_cast<float*>(base + p->off_gain), s.r3,
+                               s.dtype, st)) != hipSuccess)
+    return hip_fail(e, "pack inner_norm.weight");
+  if ((e = tmoe::launch_to_f32(U_expert, reinterpret_cast<float*>(base + p->off_uexp),
+                               s.E * s.r1, s.dtype, st)) != hipSuccess)
+    return hip_fail(e, "pack U_expert");
+  if ((e = tmoe::launch_transpose(core, base + p->off_core, s.r1 * s.r3, s.r2, es, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack core");
+  if ((e = tmoe::launch_transpose(U_out, base + p->off_uout, s.r2, s.d_out, es, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack U_out");
+  if ((e = tmoe::launch_to_f32(bias, reinterpret_cast<float*>(base + p->off_bias), s.d_out,
+                               s.dtype, st)) != hipSuccess)
+    return hip_fail(e, "pack bias");
+  return TMOE_OK;
+}
+
+int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
+                 int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!p) return fail(TMOE_EINVAL, "tmoe_forward: null plan");
+  if (T < 0) return fail(TMOE_EINVAL, "tmoe_forward: T=%lld < 0", (long long)T);
+  if (T > (int64_t)1 << 30) return fail(TMOE_EUNSUPPORTED, "tmoe_forward: T=%lld too large",
+                                        (long long)T);
+  if (T == 0) return TMOE_OK;
+  if (!x || !packed || !out || !workspace)
+    return fail(TMOE_EINVAL, "tmoe_forward: null x/packed/out/workspace");
+  if (!aligned16(x) || !aligned16(packed) || !aligned16(workspace) || !aligned16(out))
+    return fail(TMOE_EINVAL, "tmoe_forward: x/packed/out/workspace must be 16-byte aligned");
+  const Layout L = workspace_layout(p, T);
+  if (workspace_bytes < L.total)
+    return fail(TMOE_EINVAL, "tmoe_forward: workspace of %zu bytes, %zu needed for T=%lld",
+                workspace_bytes, L.total, (long long)T);
+  const tmoe_shape& s = p->s;
+  const char* pk = static_cast<const char*>(packed);
+  char* ws = static_cast<char*>(workspace);
+
+  tmoe::FwdArgs a{};
+  a.dtype = s.dtype;
+  a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
+  a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
+  a.x = x;
+  a.wr = pk + p->off_wr;
+  a.uinT = pk + p->off_uin;
+  a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
+  a.uexp = reinterpret_cast<const float*>(pk + p->off_uexp);
+  a.coreT = pk + p->off_core;
+  a.uoutT = pk + p->off_uout;
+  a.bias = reinterpret_cast<const float*>(pk + p->off_bias);
+  a.out = out;
+  a.idx = topk_idx ? topk_idx : reinterpret_cast<int32_t*>(ws + L.idx);
+  a.w = topk_w ? topk_w : reinterpret_cast<float*>(ws + L.w);
+  a.logits = logits;
+  a.c = reinterpret_cast<float*>(ws + L.c);
+  a.z = ws + L.z;
+  a.mid = ws + L.mid;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t (*const stages[kStages])(const tmoe::FwdArgs&, hipStream_t) = {
+      tmoe::launch_router, tmoe::launch_inproj, tmoe::launch_core, tmoe::launch_outproj};
+  const char* stage_names[kStages] = {"router", "in-projection", "core", "out-projection"};
+
+  std::vector<hipEvent_t> ev;
+  std::unique_lock<std::mutex> lk(g_prof.mu);
+  const bool prof = g_prof.on;
+  if (!prof) lk.unlock();
+  for (int i = 0; i < kStages; ++i) {
+    if (prof) {
+      hipEvent_t e = prof_event();
+      if (!e || hipEventRecord(e, st) != hipSuccess) return fail(TMOE_EHIP, "profiling event");
+      ev.push_back(e);
+    }
+    const hipError_t e = stages[i](a, st);
+    if (e != hipSuccess) return hip_fail(e, stage_names[i]);
+  }
+  if (prof) {
+    hipEvent_t e = prof_event();
+    if (!e || hipEventRecord(e, st) != hipSuccess) return fail(TMOE_EHIP, "profiling event");
+    ev.push_back(e);
+    g_prof.pending.push_back(std::move(ev));
+  }
+  return TMOE_OK;
+}
+
+int tmoe_prof_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof.mu);
+  g_prof.on = on != 0;
+  return TMOE_OK;
+}
+
+int tmoe_prof_read(double* ms, int n, int64_t* calls) {
+  g_err[0] = 0;
+  std::lock_guard<std::mutex> lk(g_prof.mu);
+  for (int i = 0; i < n && ms; ++i) ms[i] = 0.0;
+  int64_t count = 0;
+  int rc = kStages;
+  for (auto& ev : g_prof.pending) {
+    if (rc == kStages) {
+      const hipError_t e = hipEventSynchronize(ev.back());
+      if (e != hipSuccess) rc = hip_fail(e, "tmoe_prof_read");
+    }
+    if (rc == kStages) {
+      for (int i = 0; i < kStages && i < n && ms; ++i) {
+        float t = 0.f;
+        if (hipEventElapsedTime(&t, ev[i], ev[i + 1]) == hipSuccess) ms[i] += t;
+      }
+      ++count;
+    }
+    for (hipEvent_t e : ev) g_prof.free_ev.push_back(e);
+  }
+  g_prof.pending.clear();
+  if (calls) *calls = count;
+  return rc;
+}
+
+}  // extern "C"

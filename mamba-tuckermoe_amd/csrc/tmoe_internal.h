@@ -1,0 +1,61 @@
+// Internal interface between the C-ABI host code (tmoe_api.cpp) and the gfx950
+// kernels (tmoe_kernels.hip). Not installed; the public ABI is include/tmoe.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tmoe {
+
+// Tile geometry shared by the host (workspace / grid sizing, validation) and
+// the kernels. K-direction tiles are 128 bytes of one operand row: 64 bf16 or
+// 32 f32 elements.
+constexpr int kTileKBytes = 128;
+constexpr int kRouterBM = 64;   // tokens per router work-group
+constexpr int kInBM = 64;       // tokens per in-projection work-group (full r3 row)
+constexpr int kCoreBM = 256, kCoreBN = 128;
+constexpr int kOutBM = 256, kOutBN = 128;
+constexpr int kMaxTopK = 16;
+constexpr int kMaxExperts = 256;
+
+// Device pointers of one forward, resolved by the host.
+struct FwdArgs {
+  int dtype;                    // TMOE_BF16 / TMOE_F32
+  int64_t T, d_in, d_out, E, E_pad, k, r1, r2, r3;
+  float eps;
+  const void* x;
+  // packed weights
+  const void* wr;               // (E_pad, d_in)        router rows, zero-padded
+  const void* uinT;             // (r3, d_in)           U_in transposed
+  const float* gain;            // (r3)                 inner_norm.weight
+  const float* uexp;            // (E, r1)              U_expert
+  const void* coreT;            // (r2, r1*r3)          core as (r1*r3, r2), transposed
+  const void* uoutT;            // (d_out, r2)          U_out transposed
+  const float* bias;            // (d_out)
+  // outputs / workspace
+  void* out;
+  int32_t* idx;                 // (T, k)
+  float* w;                     // (T, k)
+  float* logits;                // (T, E) or null
+  float* c;                     // (T, r1)
+  void* z;                      // (T, r3)
+  void* mid;                    // (T, r2)
+};
+
+// Each launcher enqueues one kernel on `stream` and returns hipGetLastError().
+hipError_t launch_router(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_inproj(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
+
+// Weight packing helpers (stream-ordered).
+// dst(cols, rows) = src(rows, cols)^T, element size es (2 or 4 bytes).
+hipError_t launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int es,
+                            hipStream_t stream);
+// dst[i] = i < n ? src[i] : 0 over n_pad elements, same element size.
+hipError_t launch_copy_pad(const void* src, void* dst, int64_t n, int64_t n_pad, int es,
+                           hipStream_t stream);
+// dst[i] = float(src[i]) for n elements of dtype (TMOE_BF16 / TMOE_F32).
+hipError_t launch_to_f32(const void* src, float* dst, int64_t n, int dtype, hipStream_t stream);
+
+}  // namespace tmoe

@@ -1,0 +1,118 @@
+"""The C-ABI library: loads, exports every symbol include/tmoe.h declares, and
+rejects bad arguments on the host before any GPU call (so these run anywhere)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    src = open(os.path.join(ROOT, "include", "tmoe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(tmoe_[a-z_]+)\s*\(", src)))
+
+
+def test_exports_every_header_symbol(pkg):
+    L = pkg._lib.lib()
+    declared = _header_functions()
+    assert set(declared) == set(pkg._lib.EXPORTED)
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_abi_version(pkg):
+    assert pkg._lib.lib().tmoe_abi_version() == pkg._lib.ABI_VERSION
+
+
+def _shape(pkg, **kw):
+    d = dict(d_in=512, d_out=1024, E=8, k=2, r1=4, r2=256, r3=128, dtype=pkg._lib.TMOE_F32,
+             eps=1e-5)
+    d.update(kw)
+    return pkg._lib.TmoeShape(**d)
+
+
+def _create(pkg, **kw):
+    L = pkg._lib.lib()
+    p = ctypes.c_void_p()
+    rc = L.tmoe_plan_create(ctypes.byref(_shape(pkg, **kw)), ctypes.byref(p))
+    return rc, p, L.tmoe_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(k=9), -1, "exceeds the number of experts"),
+    (dict(k=0), -1, "positive"),
+    (dict(d_in=-1), -1, "positive"),
+    (dict(dtype=7), -1, "dtype"),
+    (dict(eps=-1.0), -1, "eps"),
+    (dict(d_in=100), -2, "d_in"),
+    (dict(r3=96), -2, "r3"),
+    (dict(r2=100), -2, "r2"),
+    (dict(d_out=1000), -2, "d_out"),
+    (dict(E=300, k=2), -2, "E=300"),
+    (dict(E=32, k=17), -2, "top_k=17"),
+    (dict(r1=65), -2, "r1"),
+])
+def test_plan_create_rejects(pkg, kw, code, msg):
+    rc, p, err = _create(pkg, **kw)
+    assert rc == code and msg in err and not p.value
+
+
+def test_plan_sizes(pkg):
+    rc, p, _ = _create(pkg)
+    L = pkg._lib.lib()
+    assert rc == 0
+    try:
+        assert L.tmoe_workspace_bytes(p, 0) == 0
+        ws64 = L.tmoe_workspace_bytes(p, 64)
+        assert ws64 >= 64 * (128 * 4 + 4 * 4 + 2 * 4 + 2 * 4 + 256 * 4)
+        assert L.tmoe_workspace_bytes(p, 128) > ws64
+        assert L.tmoe_workspace_bytes(p, -1) == 0
+        pb = L.tmoe_packed_bytes(p)
+        # every weight once (router rows padded to 16), f32
+        assert pb >= 4 * (16 * 512 + 512 * 128 + 128 + 8 * 4 + 4 * 128 * 256 + 256 * 1024 + 1024)
+    finally:
+        L.tmoe_plan_destroy(p)
+
+
+def test_forward_validation_never_launches(pkg):
+    """Every argument error is returned before the first HIP call."""
+    rc, p, _ = _create(pkg)
+    L = pkg._lib.lib()
+    fwd = L.tmoe_forward
+    ok = 0x10000   # 16-byte aligned dummy addresses, never dereferenced
+    ws = L.tmoe_workspace_bytes(p, 64)
+    try:
+        assert fwd(None, ok, 64, ok, ok, None, None, None, ok, ws, None) == -1
+        assert fwd(p, ok, -1, ok, ok, None, None, None, ok, ws, None) == -1
+        assert fwd(p, ok, 0, None, None, None, None, None, None, 0, None) == 0   # T == 0: no-op
+        assert fwd(p, None, 64, ok, ok, None, None, None, ok, ws, None) == -1
+        assert fwd(p, ok, 64, ok, None, None, None, None, ok, ws, None) == -1
+        assert fwd(p, ok + 4, 64, ok, ok, None, None, None, ok, ws, None) == -1
+        assert "aligned" in L.tmoe_last_error().decode()
+        assert fwd(p, ok, 64, ok, ok, None, None, None, ok, ws - 1, None) == -1
+        assert "workspace" in L.tmoe_last_error().decode()
+        assert fwd(p, ok, 1 << 31, ok, ok, None, None, None, ok, ws, None) == -2
+        pk = L.tmoe_pack_weights
+        assert pk(p, ok, ok, ok, None, ok, ok, ok, ok, None) == -1
+        assert "U_expert" in L.tmoe_last_error().decode()
+        assert pk(p, ok, ok, ok, ok, ok, ok, ok, ok + 8, None) == -1
+        assert pk(None, ok, ok, ok, ok, ok, ok, ok, ok, None) == -1
+    finally:
+        L.tmoe_plan_destroy(p)
+
+
+def test_plan_wrapper_raises(pkg):
+    with pytest.raises(pkg._lib.TmoeError) as e:
+        pkg._lib.Plan(512, 1024, 8, 9, 4, 256, 128, torch.float32, 1e-5)
+    assert e.value.code == -1
+    with pytest.raises(pkg._lib.TmoeError):
+        pkg._lib.Plan(512, 1024, 8, 2, 4, 256, 128, torch.float16, 1e-5)
+
+
+def test_prof_read_empty(pkg):
+    ms, calls = pkg._lib.prof_read()
+    assert calls == 0 and ms == [0.0] * pkg._lib.N_STAGES

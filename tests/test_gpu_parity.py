@@ -1,0 +1,158 @@
+"""Parity of the gfx950 path (through the C ABI) with the CPU oracle.
+
+Bar (north star): top-k indices bit-exact; outputs within rel-L2 <= 1e-5 (fp32)
+and <= 1e-2 (bf16) of the reference's PyTorch path. For bf16 workloads the
+reference path is run in float32 on the bf16-valued inputs (fp32 router logits),
+which is oracle/tucker_moe_torch.forward(compute_dtype=float32).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tucker_moe_np as onp
+from oracle import tucker_moe_torch as ot
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
+
+
+def _module(pkg, dev, w, params):
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
+    m.load_state_dict({k: v.to(dev) for k, v in params.items()})
+    return m
+
+
+def _run(m, x, dev):
+    with torch.no_grad():
+        out, idx, wts, lg = m.forward_with_routing(x.to(dev), logits=True)
+    torch.cuda.synchronize()
+    return out.float().cpu(), idx.cpu(), wts.cpu(), lg.cpu()
+
+
+def _check(w, got, ref64, label, torch_ref=None):
+    out, idx, wts, lg = got
+    T = out.shape[0]
+    gaps = onp.topk_gap(ref64["logits"][:T], w.k)
+    mism = np.nonzero((idx.numpy() != ref64["idx"][:T]).any(1))[0]
+    lg_err = onp.rel_l2(lg.numpy(), ref64["logits"][:T])
+    err64 = onp.rel_l2(out.numpy(), ref64["out"][:T])
+    msg = (f"{label}: T={T} rel_l2(out, f64)={err64:.3e} rel_l2(logits)={lg_err:.3e} "
+           f"min_topk_gap={gaps.min():.3e} routing_mismatch_rows={len(mism)}")
+    if torch_ref is not None:
+        n = torch_ref["out"].shape[0]
+        err_t = onp.rel_l2(out[:n].numpy(), torch_ref["out"].double().numpy())
+        same_t = torch.equal(idx[:n], torch_ref["idx"])
+        msg += f" rel_l2(out, torch fp32 ref)={err_t:.3e} routing_equal_torch={same_t}"
+    print(msg, flush=True)
+    assert len(mism) == 0, f"{msg}; rows {mism[:8]} gaps {gaps[mism[:8]]}"
+    assert lg_err < (1e-6 if w.dtype == torch.float32 else 1e-5), msg
+    assert np.abs(wts.numpy() - ref64["w"][:T]).max() < 1e-5, msg
+    assert err64 <= TOL[w.dtype], msg
+    if torch_ref is not None:
+        assert same_t and err_t <= TOL[w.dtype], msg
+
+
+@pytest.mark.parametrize("name,T", [("C1", 64), ("C2", 32), ("C3", 1024), ("C4", 512)])
+@pytest.mark.parametrize("affine", ["unit", "random"])
+def test_workload_parity(pkg, dev, name, T, affine):
+    w = pkg.WORKLOADS[name]
+    params = pkg.synth.make_params(w, affine=affine)
+    x = pkg.synth.make_x(w, T)
+    got = _run(_module(pkg, dev, w, params), x, dev)
+    ref64 = onp.forward_f64(x, params, w.k)
+    tref = ot.forward(x, params, w.k, compute_dtype=torch.float32, intermediates=True)
+    _check(w, got, ref64, f"{name}/{affine}", tref)
+
+
+@pytest.mark.parametrize("name", ["C3", "C4"])
+def test_full_size(pkg, dev, name):
+    """BASELINE's full T, against the float64 oracle on every token and the
+    torch fp32 restatement on the first 512."""
+    w = pkg.WORKLOADS[name]
+    params = pkg.synth.make_params(w)
+    x = pkg.synth.make_x(w)
+    got = _run(_module(pkg, dev, w, params), x, dev)
+    ref64 = onp.forward_f64(x, params, w.k)
+    tref = ot.forward(x[:512], params, w.k, compute_dtype=torch.float32, intermediates=True)
+    _check(w, got, ref64, f"{name}/full", tref)
+
+
+@pytest.mark.parametrize("T", [1, 3, 63, 65, 255, 257, 1000])
+@pytest.mark.parametrize("name", ["C1", "C2"])
+def test_ragged_tokens(pkg, dev, name, T):
+    w = pkg.WORKLOADS[name]
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, T, stream=3)
+    got = _run(_module(pkg, dev, w, params), x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"{name}/T={T}")
+
+
+SHAPES = [
+    # (E, k, r1, r3, r2, d_in, d_out)
+    (1, 1, 4, 128, 256, 256, 512),      # E = k = 1: dense chain
+    (16, 16, 4, 256, 512, 512, 256),    # k = E: every expert
+    (32, 3, 2, 64, 128, 128, 96),       # r3 = 64, E_pad 32
+    (100, 5, 8, 128, 192, 320, 160),    # E_pad 128, odd k
+    (64, 4, 1, 256, 64, 64, 64),        # r1 = 1, tiny r2
+    (8, 2, 32, 256, 512, 768, 4608),    # the reference's default ranks (config.py:20-24)
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "E%d_k%d_r%d-%d-%d_%dx%d" % s)
+def test_shapes(pkg, dev, shape, dtype):
+    E, k, r1, r3, r2, d_in, d_out = shape
+    w = pkg.Workload("custom", 200, d_in, d_out, E, k, r1, r3, r2, dtype, 77)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    got = _run(_module(pkg, dev, w, params), x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"shape {shape} {dtype}")
+
+
+def test_deterministic_and_batch_dims(pkg, dev):
+    w = pkg.WORKLOADS["C2"]
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, 60).to(dev)
+    m = _module(pkg, dev, w, params)
+    with torch.no_grad():
+        a = m(x)
+        b = m(x.reshape(3, 4, 5, w.d_in))
+        c = m(x)
+    assert b.shape == (3, 4, 5, w.d_out)
+    assert torch.equal(a, c) and torch.equal(a, b.reshape(60, w.d_out))
+
+
+def test_repack_after_parameter_update(pkg, dev):
+    w = pkg.WORKLOADS["C1"]
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, 16)
+    m = _module(pkg, dev, w, params)
+    with torch.no_grad():
+        m(x.to(dev))
+        m.bias.add_(1.0)      # moves the version counter: repacked automatically
+        out = m(x.to(dev)).cpu()
+    p2 = dict(params)
+    p2["bias"] = params["bias"] + 1.0
+    assert onp.rel_l2(out.numpy(), onp.forward_f64(x, p2, w.k)["out"]) < 1e-5
+    m.U_out.data.mul_(0.0)    # .data writes need refresh_packed()
+    m.refresh_packed()
+    with torch.no_grad():
+        out = m(x.to(dev)).cpu()
+    assert torch.allclose(out, p2["bias"].expand_as(out))
+
+
+def test_side_stream(pkg, dev):
+    w = pkg.WORKLOADS["C2"]
+    params = pkg.synth.make_params(w)
+    x = pkg.synth.make_x(w, 40).to(dev)
+    m = _module(pkg, dev, w, params)
+    with torch.no_grad():
+        ref = m(x)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            out = m(x)
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

@@ -1,0 +1,243 @@
+"""Pins the CPU oracle (oracle/) with checks the mathematics fixes.
+
+The reference ships no golden vectors for this path, so the oracle is pinned by:
+two independent formulations agreeing (torch op-for-op restatement vs float64
+regrouped algebra vs pure-Python brute force), closed forms and special cases,
+and planted mistakes that at least one check must catch.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tucker_moe_np as onp
+from oracle import tucker_moe_torch as ot
+
+
+def _params(seed, E, d_in, d_out, r1, r3, r2, affine=True):
+    g = torch.Generator().manual_seed(seed)
+    n = lambda *s, std=1.0: torch.randn(*s, generator=g) * std
+    p = {
+        "router.weight": n(E, d_in, std=d_in ** -0.5),
+        "U_in": n(d_in, r3, std=d_in ** -0.5),
+        "inner_norm.weight": 1 + 0.1 * n(r3) if affine else torch.ones(r3),
+        "U_expert": n(E, r1),
+        "core": n(r1, r3, r2, std=(r1 * r3) ** -0.5),
+        "U_out": n(r2, d_out, std=r2 ** -0.5),
+        "bias": 0.1 * n(d_out) if affine else torch.zeros(d_out),
+    }
+    return p
+
+
+def _x(seed, T, d_in):
+    return torch.randn(T, d_in, generator=torch.Generator().manual_seed(seed + 7))
+
+
+SMALL = dict(E=6, d_in=24, d_out=20, r1=3, r3=16, r2=12)
+
+
+def check_suite(forward, top_k=2, seed=0):
+    """The pinning checks, parametrised by the forward under test.
+    Returns a list of (name, passed)."""
+    res = []
+    d = SMALL
+    p = _params(seed, **d)
+    x = _x(seed, 9, d["d_in"])
+    out = forward(x, p, top_k)
+    ref = onp.forward_f64(x, p, top_k)
+    res.append(("f64 agreement", onp.rel_l2(out, ref["out"]) < 1e-5))
+    bf = onp.brute_force(x[:3], p, top_k)
+    res.append(("brute force", onp.rel_l2(out[:3], bf) < 1e-5))
+    # E = k = 1: dense low-rank chain RMSNorm(x U_in) (U_expert[0] . core) U_out + b
+    p1 = _params(seed + 1, E=1, d_in=d["d_in"], d_out=d["d_out"], r1=d["r1"], r3=d["r3"], r2=d["r2"])
+    o1 = forward(x, p1, 1).double()
+    pd = {k: v.double() for k, v in p1.items()}
+    zr = x.double() @ pd["U_in"]
+    z = zr / torch.sqrt((zr * zr).mean(-1, keepdim=True) + 1e-5) * pd["inner_norm.weight"]
+    G = torch.einsum("r,rst->st", pd["U_expert"][0], pd["core"])
+    dense = z @ G @ pd["U_out"] + pd["bias"]
+    res.append(("E=k=1 dense chain", onp.rel_l2(o1, dense) < 1e-5))
+    # one-hot U_expert with E = r1: expert e uses core[e]
+    po = _params(seed + 2, E=d["r1"], d_in=d["d_in"], d_out=d["d_out"], r1=d["r1"], r3=d["r3"],
+                 r2=d["r2"])
+    po["U_expert"] = torch.eye(d["r1"])
+    oo = forward(x, po, 2).double()
+    pd = {k: v.double() for k, v in po.items()}
+    S = x.double() @ pd["router.weight"].T
+    v, e = torch.topk(S, 2, dim=-1)
+    wts = torch.softmax(v, -1)
+    zr = x.double() @ pd["U_in"]
+    z = zr / torch.sqrt((zr * zr).mean(-1, keepdim=True) + 1e-5) * pd["inner_norm.weight"]
+    moe = sum(wts[:, j:j + 1] * torch.einsum("ts,tsq->tq", z, pd["core"][e[:, j]]) for j in range(2))
+    res.append(("one-hot experts", onp.rel_l2(oo, moe @ pd["U_out"] + pd["bias"]) < 1e-5))
+    # k = 1: out(a x) == out(x) for a > 0
+    o_a = forward(3.0 * x, p, 1)
+    o_b = forward(x, p, 1)
+    res.append(("k=1 scale invariance", onp.rel_l2(o_a, o_b) < 1e-5))
+    # U_out = 0 -> bias
+    pz = dict(p)
+    pz["U_out"] = torch.zeros_like(p["U_out"])
+    oz = forward(x, pz, top_k)
+    res.append(("U_out=0 gives bias", torch.equal(oz, p["bias"].expand_as(oz).to(oz.dtype))))
+    # linearity of (out - bias) in core with routing fixed (routing does not read core)
+    pa, pb, pab = dict(p), dict(p), dict(p)
+    c2 = _params(seed + 3, **d)["core"]
+    pb["core"] = c2
+    pab["core"] = p["core"] + c2
+    la = forward(x, pa, top_k) - p["bias"]
+    lb = forward(x, pb, top_k) - p["bias"]
+    lab = forward(x, pab, top_k) - p["bias"]
+    res.append(("linear in core", onp.rel_l2(la + lb, lab) < 1e-5))
+    # linearity in U_out
+    pu = dict(p)
+    pu["U_out"] = 2.0 * p["U_out"]
+    res.append(("linear in U_out",
+                onp.rel_l2(forward(x, pu, top_k) - p["bias"], 2 * (out - p["bias"])) < 1e-5))
+    # token permutation equivariance
+    perm = torch.randperm(x.shape[0], generator=torch.Generator().manual_seed(5))
+    res.append(("permutation equivariance", onp.rel_l2(forward(x[perm], p, top_k), out[perm]) < 1e-6))
+    return res
+
+
+def torch_forward(x, p, k):
+    return ot.forward(x, p, k, chunk=4)
+
+
+def np_forward(x, p, k):
+    return torch.from_numpy(onp.forward_f64(x, p, k)["out"]).float()
+
+
+@pytest.mark.parametrize("fwd", [torch_forward, np_forward], ids=["torch", "f64"])
+@pytest.mark.parametrize("top_k", [1, 2, 3])
+def test_oracle_passes_all_checks(fwd, top_k):
+    res = check_suite(fwd, top_k=top_k)
+    failed = [n for n, ok in res if not ok]
+    assert not failed, failed
+
+
+def test_intermediates_agree():
+    d = dict(E=8, d_in=64, d_out=48, r1=4, r3=32, r2=40)
+    p = _params(11, **d)
+    x = _x(11, 70, 64)
+    a = ot.forward(x, p, 2, chunk=16, intermediates=True)
+    b = onp.forward_f64(x, p, 2)
+    assert np.array_equal(a["idx"].numpy(), b["idx"])
+    for k in ("logits", "w", "z", "mid", "out"):
+        assert onp.rel_l2(a[k].numpy(), b[k]) < 1e-5, k
+    np.testing.assert_allclose(b["w"].sum(1), 1.0, rtol=1e-12)
+    assert np.all(np.diff(np.take_along_axis(b["logits"], b["idx"], 1), axis=1) <= 0)
+
+
+def test_chunking_is_exact():
+    d = dict(E=8, d_in=64, d_out=48, r1=4, r3=32, r2=40)
+    p = _params(12, **d)
+    x = _x(12, 37, 64)
+    a = ot.forward(x, p, 2, chunk=5)
+    b = ot.forward(x, p, 2, chunk=1000)
+    assert onp.rel_l2(a, b) < 1e-6
+
+
+def test_batch_dims_flatten():
+    d = dict(E=8, d_in=64, d_out=48, r1=4, r3=32, r2=40)
+    p = _params(13, **d)
+    x = _x(13, 12, 64)
+    a = ot.forward(x.reshape(3, 4, 64), p, 2)
+    assert a.shape == (3, 4, 48)
+    assert torch.equal(a.reshape(12, 48), ot.forward(x, p, 2))
+
+
+def test_rmsnorm_closed_form():
+    c, n, eps = 0.7, 16, 1e-5
+    z = torch.full((2, n), c, dtype=torch.float64)
+    w = torch.linspace(0.5, 1.5, n, dtype=torch.float64)
+    out = ot.rmsnorm(z, w, eps)
+    expect = c / math.sqrt(c * c + eps) * w
+    assert torch.allclose(out, expect.expand_as(out), rtol=1e-14)
+
+
+def test_topk_matches_stable_argsort():
+    g = torch.Generator().manual_seed(3)
+    S = torch.randn(500, 16, generator=g)
+    v, i = torch.topk(S, 4, dim=-1)
+    j = np.argsort(-S.numpy(), axis=1, kind="stable")[:, :4]
+    assert np.array_equal(i.numpy(), j)
+    # softmax over the k selected values only (model.py:77), closed form
+    w = torch.softmax(v.double(), -1)
+    e = torch.exp(v.double() - v[:, :1].double())
+    assert torch.allclose(w, e / e.sum(-1, keepdim=True), rtol=1e-12)
+
+
+def test_topk_gap():
+    S = np.array([[3.0, 1.0, 2.0, 0.5], [1.0, 1.0, 1.0, 0.0]])
+    np.testing.assert_allclose(onp.topk_gap(S, 2), [1.0, 0.0])
+    assert np.isinf(onp.topk_gap(S, 4)).all()
+
+
+# ---- planted mistakes: each must fail at least one check ---------------------
+
+def _mut_softmax_over_all(xf, router_w, top_k):
+    # softmax over all E logits, then top-k (the trained-model router's order)
+    scores = torch.nn.functional.linear(xf, router_w)
+    probs = torch.softmax(scores, -1)
+    v, i = torch.topk(probs, top_k, dim=-1)
+    return scores, i, v
+
+
+def _mut_no_eps_inside(xf, U_in, inner_w, eps):
+    z = xf @ U_in
+    return z / (z.pow(2).mean(-1, keepdim=True).sqrt() + 1.0) * inner_w
+
+
+def _mut_rsqrt_missing_mean(xf, U_in, inner_w, eps):
+    z = xf @ U_in
+    return z / z.pow(2).sum(-1, keepdim=True).add(eps).sqrt() * inner_w
+
+
+def _mut_first_slot_only(z, idx, w, U_expert, core):
+    return ot.core_contract(z, idx[:, :1], w[:, :1] * 0 + 1, U_expert, core)
+
+
+def _mut_weights_swapped(z, idx, w, U_expert, core):
+    return ot.core_contract(z, idx, w.flip(1), U_expert, core)
+
+
+def _mut_core_transposed(z, idx, w, U_expert, core):
+    # use core[r] transposed on the (r3, r2) face: only typechecks when r3 == r2,
+    # so apply it to a square slice and pad
+    r1, r3, r2 = core.shape
+    n = min(r3, r2)
+    c = core.clone()
+    c[:, :n, :n] = core[:, :n, :n].transpose(1, 2)
+    return ot.core_contract(z, idx, w, U_expert, c)
+
+
+def _mut_bias_dropped(mid, U_out, bias):
+    return mid @ U_out
+
+
+def _mut_no_gain(xf, U_in, inner_w, eps):
+    return ot.rmsnorm(xf @ U_in, torch.ones_like(inner_w), eps)
+
+
+MUTANTS = {
+    "softmax over all E": {"route": _mut_softmax_over_all},
+    "eps outside sqrt": {"project_in": _mut_no_eps_inside},
+    "sum instead of mean": {"project_in": _mut_rsqrt_missing_mean},
+    "first slot only": {"core_contract": _mut_first_slot_only},
+    "slot weights swapped": {"core_contract": _mut_weights_swapped},
+    "core face transposed": {"core_contract": _mut_core_transposed},
+    "bias dropped": {"project_out": _mut_bias_dropped},
+    "gain dropped": {"project_in": _mut_no_gain},
+}
+
+
+@pytest.mark.parametrize("name", sorted(MUTANTS))
+def test_planted_mistake_is_caught(name):
+    stages = MUTANTS[name]
+
+    def fwd(x, p, k):
+        return ot.forward(x, p, k, stages=stages)
+
+    res = check_suite(fwd, top_k=2)
+    assert any(not ok for _, ok in res), f"mutant '{name}' passed every check"
