@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Tucker-MoE layer forward throughput on one MI355X.
+
+One step = one tmoe_forward (the whole layer: router/top-k, in-projection +
+RMSNorm, core contraction, out-projection) over one batch of T synthetic tokens
+already resident in HBM. The default workload is C3 (T=16384, d_in=1536,
+d_out=2304, E=16, top-2, r=(4,256,1024), bf16), the configuration BASELINE's
+metric is quoted on.
+
+Buffer sets (tokens, outputs, workspace and a copy of the packed weights) are
+rotated so that the working set exceeds the 256 MB Infinity Cache and each step
+reads its operands from HBM.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "TuckerMoE layer tokens/sec + % bf16 MFMA peak at T=16384; vs host-CPU ref"
+PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}   # MI355X dense MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="C3")
+    ap.add_argument("--tokens", type=int, default=None, help="override T")
+    ap.add_argument("--rotate-mb", type=float, default=640.0,
+                    help="minimum total size of the rotated buffer sets")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="approximate CPU work of the host baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this "
+              "build (the layer shards by tokens with no exchange; see the design notes).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    L = pkg._lib.lib()
+
+    w = pkg.WORKLOADS[args.workload]
+    if args.tokens:
+        w = w.with_T(args.tokens)
+    if w.fp8:
+        raise SystemExit(f"workload {w.name} (fp8) is not implemented yet")
+    T = w.T
+    dev = torch.device("cuda:0")
+    dt_name = "bf16" if w.dtype == torch.bfloat16 else "f32"
+    es = 2 if w.dtype == torch.bfloat16 else 4
+
+    # -- model and rotated buffer sets -----------------------------------------
+    params = pkg.synth.make_params(w)
+    x0 = pkg.synth.make_x(w)
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
+    m.load_state_dict({k: v.to(dev) for k, v in params.items()})
+    plan = m.plan()
+    packed0 = m.packed()
+    ws_bytes = plan.workspace_bytes(T)
+    set_bytes = T * w.d_in * es + T * w.d_out * es + ws_bytes + packed0.numel()
+    n_sets = max(3, math.ceil(args.rotate_mb * 1e6 / set_bytes))
+    log(f"[bench] workload {w.name}: T={T} d_in={w.d_in} d_out={w.d_out} E={w.E} k={w.k} "
+        f"r=({w.r1},{w.r3},{w.r2}) {dt_name}; {n_sets} rotated sets x {set_bytes / 1e6:.1f} MB")
+    gen = torch.Generator(device=dev).manual_seed(w.seed)
+    sets = []
+    for i in range(n_sets):
+        x = x0.to(dev) if i == 0 else torch.randn(T, w.d_in, device=dev, generator=gen).to(w.dtype)
+        pk = packed0 if i == 0 else packed0.clone()
+        sets.append(dict(
+            x=x, pk=pk,
+            out=torch.empty(T, w.d_out, dtype=w.dtype, device=dev),
+            ws=torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)))
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+
+    def step(i):
+        s = sets[i % n_sets]
+        rc = L.tmoe_forward(plan.ptr, s["x"].data_ptr(), T, s["pk"].data_ptr(), s["out"].data_ptr(),
+                            None, None, None, s["ws"].data_ptr(), ws_bytes, sptr)
+        if rc != 0:
+            pkg._lib.check(rc)
+
+    # -- warmup + timed region ------------------------------------------------
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / args.steps
+    tok_s = T * args.steps / (gpu_ms / 1e3)
+    log(f"[bench] {args.steps} steps: {gpu_ms:.3f} ms on the stream ({wall * 1e3:.3f} ms wall), "
+        f"{ms_per_step * 1e3:.2f} us/step, {tok_s / 1e6:.2f} M tok/s")
+
+    # -- per-stage kernel durations (HIP events recorded by the library) ---------
+    pkg._lib.prof_enable(True)
+    try:
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        stage_ms, calls = pkg._lib.prof_read()
+    finally:
+        pkg._lib.prof_enable(False)
+    stage_avg_us = {n: stage_ms[j] / calls * 1e3 for j, n in enumerate(pkg._lib.STAGE_NAMES)}
+    fl = w.flops()
+    dom = max(stage_avg_us, key=stage_avg_us.get)
+    dom_tflops = fl[dom] / (stage_avg_us[dom] * 1e-6) / 1e12
+    peak = PEAK_TFLOPS[dt_name]
+    layer_tflops = fl["total"] / (ms_per_step * 1e-3) / 1e12
+    log("[bench] per-stage avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in stage_avg_us.items()))
+    log(f"[bench] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak; "
+        f"layer {layer_tflops:.1f} TFLOP/s = {layer_tflops / peak:.3f} of peak")
+
+    traffic = None
+    tr_path = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
+    if os.path.exists(tr_path) and T == pkg.WORKLOADS[w.name].T:
+        with open(tr_path) as f:
+            traffic = json.load(f).get(dom)
+
+    # -- parity on a slice (GPU result of set 0 vs the fp32 reference path) --------
+    from oracle import tucker_moe_np as onp
+    from oracle import tucker_moe_torch as ot
+    n_par = min(T, 512)
+    s0 = sets[0]
+    idx = torch.empty(T, w.k, dtype=torch.int32, device=dev)
+    pkg._lib.check(L.tmoe_forward(plan.ptr, s0["x"].data_ptr(), T, s0["pk"].data_ptr(),
+                                  s0["out"].data_ptr(), idx.data_ptr(), None, None,
+                                  s0["ws"].data_ptr(), ws_bytes, sptr))
+    torch.cuda.synchronize()
+    ref = ot.forward(x0[:n_par], params, w.k, compute_dtype=torch.float32, intermediates=True)
+    parity = {
+        "tokens": n_par,
+        "rel_l2_out": onp.rel_l2(s0["out"][:n_par].float().cpu().numpy(), ref["out"].double().numpy()),
+        "topk_idx_equal": bool(torch.equal(idx[:n_par].long().cpu(), ref["idx"])),
+        "min_topk_gap": float(onp.topk_gap(ref["logits"].double().numpy(), w.k).min()),
+        "reference": "oracle/tucker_moe_torch fp32 on the bf16-valued inputs",
+    }
+    log(f"[bench] parity on {n_par} tokens: {parity}")
+
+    # -- host-CPU baseline (rank 0, N=1): the reference op sequence on the CPU --------
+    cpu = None
+    if not args.no_cpu:
+        threads = torch.get_num_threads()
+        chunk = 512
+        xs = x0[:chunk]
+        t_a = time.perf_counter()
+        ot.forward(xs, params, w.k, chunk=chunk)            # warm-up, also sizes the sample
+        rate = chunk / (time.perf_counter() - t_a)
+        n_cpu = int(min(T, max(chunk, args.cpu_seconds * rate)) // chunk * chunk)
+        t_a = time.perf_counter()
+        ot.forward(x0[:n_cpu], params, w.k, chunk=chunk)
+        cpu_s = time.perf_counter() - t_a
+        cpu = {
+            "value": n_cpu / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"first {n_cpu} of the {T} {w.name} tokens, {dt_name} tensors, "
+                       f"reference op sequence (oracle/tucker_moe_torch), chunks of {chunk}, "
+                       f"torch {torch.__version__} with {threads} threads on {cpu_model()}"),
+            "seconds": cpu_s,
+        }
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s on {threads} threads ({n_cpu} tokens, {cpu_s:.1f} s)")
+
+    res = {
+        "metric": METRIC,
+        "value": tok_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt_name,
+        "data": "synthetic (seeded N(0,1) tokens, N(0,1/fan_in) weights; no checkpoint)",
+        "config": {"workload": f"{w.name}: Tucker-MoE layer forward, one GPU", "T": T,
+                   "d_in": w.d_in, "d_out": w.d_out, "E": w.E, "top_k": w.k,
+                   "r1": w.r1, "r3": w.r3, "r2": w.r2, "rotated_sets": n_sets},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,
+                     "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
+                     "avg_us": stage_avg_us[dom], "flops_per_launch": fl[dom]},
+        "layer": {"tflops": layer_tflops, "mfma_frac": layer_tflops / peak,
+                  "hbm_gbs_compulsory": w.hbm_bytes() / (ms_per_step * 1e-3) / 1e9,
+                  "stage_avg_us": stage_avg_us},
+        "parity": parity,
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": (tok_s / cpu["value"]) if cpu else None,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
