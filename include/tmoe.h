@@ -110,7 +110,7 @@ int tmoe_forward(const tmoe_plan* plan, const void* x, int64_t T, const void* pa
  * While enabled, every tmoe_forward records a HIP event before each of its
  * kernels and one after the last, on the forward's stream. tmoe_prof_read waits
  * for those events, writes the summed milliseconds per stage into ms[0..n-1]
- * (stage order: router, in-projection, core, out-projection), the number of
+ * (stage order: front = router + in-projection, core, out-projection), the number of
  * forwards into *calls, and clears the record. Returns the stage count. Not
  * thread-safe; for benchmarks only. */
 int tmoe_prof_enable(int on);

@@ -22,8 +22,8 @@ LIB_PATH = os.path.join(HERE, "libtmoe.so")
 ABI_VERSION = 1
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16 = 0, 1
-N_STAGES = 4
-STAGE_NAMES = ("router", "in_proj", "core", "out_proj")
+N_STAGES = 3
+STAGE_NAMES = ("front", "core", "out_proj")
 
 # Every function include/tmoe.h declares.
 EXPORTED = (

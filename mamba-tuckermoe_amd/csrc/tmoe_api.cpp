@@ -20,8 +20,9 @@ struct tmoe_plan {
   tmoe_shape s;
   int64_t E_pad;
   size_t es;   // element size of the plan dtype
-  // packed-weight layout (byte offsets)
-  size_t off_wr, off_uin, off_gain, off_uexp, off_core, off_uout, off_bias, packed_bytes;
+  // packed-weight layout (byte offsets); the front operand is U_in^T (r3 rows)
+  // immediately followed by the router rows (E_pad rows, zero past E)
+  size_t off_front, off_router, off_gain, off_uexp, off_core, off_uout, off_bias, packed_bytes;
 };
 
 namespace {
@@ -44,7 +45,7 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-constexpr int kStages = 4;
+constexpr int kStages = 3;
 
 // Per-stage event record of tmoe_prof_enable.
 struct Prof {
@@ -127,12 +128,13 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   if (!p) return fail(TMOE_EINVAL, "out of host memory");
   p->s = s;
   p->es = s.dtype == TMOE_BF16 ? 2 : 4;
-  int64_t ep = 16;
-  while (ep < s.E) ep *= 2;   // router tile widths: 16, 32, 64, 128, 256
+  int64_t ep = 32;
+  while (ep < s.E) ep *= 2;   // router column blocks of 32: widths 32, 64, 128, 256
   p->E_pad = ep;
   size_t o = 0;
-  p->off_wr = o;   o = align256(o + (size_t)p->E_pad * s.d_in * p->es);
-  p->off_uin = o;  o = align256(o + (size_t)s.r3 * s.d_in * p->es);
+  p->off_front = o;
+  p->off_router = o + (size_t)s.r3 * s.d_in * p->es;
+  o = align256(p->off_router + (size_t)p->E_pad * s.d_in * p->es);
   p->off_gain = o; o = align256(o + (size_t)s.r3 * sizeof(float));
   p->off_uexp = o; o = align256(o + (size_t)s.E * s.r1 * sizeof(float));
   p->off_core = o; o = align256(o + (size_t)s.r2 * s.r1 * s.r3 * p->es);
@@ -170,11 +172,11 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
   char* base = static_cast<char*>(packed);
   const int es = (int)p->es;
   hipError_t e;
-  if ((e = tmoe::launch_copy_pad(router_w, base + p->off_wr, s.E * s.d_in, p->E_pad * s.d_in, es,
-                                 st)) != hipSuccess)
-    return hip_fail(e, "pack router");
-  if ((e = tmoe::launch_transpose(U_in, base + p->off_uin, s.d_in, s.r3, es, st)) != hipSuccess)
+  if ((e = tmoe::launch_transpose(U_in, base + p->off_front, s.d_in, s.r3, es, st)) != hipSuccess)
     return hip_fail(e, "pack U_in");
+  if ((e = tmoe::launch_copy_pad(router_w, base + p->off_router, s.E * s.d_in,
+                                 p->E_pad * s.d_in, es, st)) != hipSuccess)
+    return hip_fail(e, "pack router");
   if ((e = tmoe::launch_to_f32(inner_w, reinterpret_cast<float*>(base + p->off_gain), s.r3,
                                s.dtype, st)) != hipSuccess)
     return hip_fail(e, "pack inner_norm.weight");
@@ -219,8 +221,7 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
   a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
   a.x = x;
-  a.wr = pk + p->off_wr;
-  a.uinT = pk + p->off_uin;
+  a.wfront = pk + p->off_front;
   a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
   a.uexp = reinterpret_cast<const float*>(pk + p->off_uexp);
   a.coreT = pk + p->off_core;
@@ -236,8 +237,9 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t (*const stages[kStages])(const tmoe::FwdArgs&, hipStream_t) = {
-      tmoe::launch_router, tmoe::launch_inproj, tmoe::launch_core, tmoe::launch_outproj};
-  const char* stage_names[kStages] = {"router", "in-projection", "core", "out-projection"};
+      tmoe::launch_front, tmoe::launch_core, tmoe::launch_outproj};
+  const char* stage_names[kStages] = {"front (router + in-projection)", "core",
+                                      "out-projection"};
 
   std::vector<hipEvent_t> ev;
   std::unique_lock<std::mutex> lk(g_prof.mu);

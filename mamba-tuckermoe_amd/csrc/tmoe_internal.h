@@ -11,10 +11,8 @@ namespace tmoe {
 // the kernels. K-direction tiles are 128 bytes of one operand row: 64 bf16 or
 // 32 f32 elements.
 constexpr int kTileKBytes = 128;
-constexpr int kRouterBM = 64;   // tokens per router work-group
-constexpr int kInBM = 64;       // tokens per in-projection work-group (full r3 row)
-constexpr int kCoreBM = 256, kCoreBN = 128;
-constexpr int kOutBM = 256, kOutBN = 128;
+constexpr int kFrontBM = 64;    // tokens per k_front work-group (whole r3 and E rows)
+constexpr int kFrontPFA = 8;    // K tiles of x in flight per k_front work-group
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 256;
 
@@ -25,8 +23,8 @@ struct FwdArgs {
   float eps;
   const void* x;
   // packed weights
-  const void* wr;               // (E_pad, d_in)        router rows, zero-padded
-  const void* uinT;             // (r3, d_in)           U_in transposed
+  const void* wfront;           // (r3 + E_pad, d_in)   U_in^T rows, then router rows
+                                //                      (zero rows past E)
   const float* gain;            // (r3)                 inner_norm.weight
   const float* uexp;            // (E, r1)              U_expert
   const void* coreT;            // (r2, r1*r3)          core as (r1*r3, r2), transposed
@@ -43,8 +41,7 @@ struct FwdArgs {
 };
 
 // Each launcher enqueues one kernel on `stream` and returns hipGetLastError().
-hipError_t launch_router(const FwdArgs& a, hipStream_t stream);
-hipError_t launch_inproj(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
 

@@ -1,0 +1,717 @@
+// gfx950 device code of the Tucker-MoE layer forward (templates; the launch
+// configurations used by the library are chosen in tmoe_kernels.hip).
+//
+// The reference computes (pure_torch_mlx/model.py:68-102), per token row x:
+//   s = x W_r^T ; (v, e) = topk(s, k) ; w = softmax(v)            model.py:75-77
+//   z = RMSNorm(x U_in) * g                                        model.py:80-81, :25-27
+//   mid = sum_j w_j * z (sum_r U_expert[e_j, r] core[r])           model.py:87-98
+//   out = mid U_out + bias                                         model.py:101
+// Here the middle line is regrouped as mid = sum_{r,s} c_r z_s core[r, s, :],
+// with c = sum_j w_j U_expert[e_j] (a (T, r1) matrix): one GEMM with
+// K = r1*r3 whose A operand c (x) z is formed while it is staged into LDS.
+//
+// Three kernels, each an MFMA GEMM over 128-byte K tiles staged through LDS:
+//   k_front   : [z | logits] = x [U_in | W_r^T]; RMSNorm epilogue on z;
+//               top-k, softmax and c epilogue on the logits (x is read once)
+//   k_core    : mid = (c (x) z) core_flat
+//   k_outproj : out = mid U_out + bias
+//
+// Operand layout: every GEMM here is "NT": A is (M, K) and B^T is (N, K), both
+// K-contiguous, so one lane of an MFMA fragment reads 16 contiguous bytes. The
+// weights are re-laid to B^T once, at pack time.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "tmoe_internal.h"
+
+namespace tmoe {
+namespace dev {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ---- element types -------------------------------------------------------
+struct EltBF16 {
+  typedef uint16_t T;   // bf16 bits
+};
+struct EltF32 {
+  typedef float T;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);   // round to nearest even
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+__device__ __forceinline__ float load_as_f32(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+__device__ __forceinline__ float load_as_f32(const float* p) { return *p; }
+__device__ __forceinline__ void store_from_f32(uint16_t* p, float v) { *p = f32_to_bf16_bits(v); }
+__device__ __forceinline__ void store_from_f32(float* p, float v) { *p = v; }
+
+// One 32x32 output block += A(32 x Ks) * B(Ks x 32), where one K step is 32
+// bytes of each operand row: lane l supplies row/column (l & 31) and the 16-byte
+// half (l >> 5) of the step.
+// bf16: one v_mfma_f32_32x32x16_bf16 (Ks = 16). On gfx950 this shape issues at
+//       the full 1024 flop/clk/SIMD; the 16x16x32 shape sustains about 60% of it.
+// f32 : four v_mfma_f32_32x32x2_f32, chunk element j feeding MFMA j (Ks = 8).
+// A and B use the same slice mapping, so any consistent K order is exact.
+// Accumulator element e of lane l holds row acc_row(l, e), column (l & 31).
+__device__ __forceinline__ int acc_row(int lane, int e) {
+  return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+__device__ __forceinline__ void mma(f32x16& acc, u32x4 a, u32x4 b, EltBF16) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x16& acc, u32x4 a, u32x4 b, EltF32) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[j]), __uint_as_float(b[j]), acc,
+                                               0, 0, 0);
+}
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) z[e] = 0.f;
+  return z;
+}
+
+// ---- operand tile loaders ------------------------------------------------
+// fetch(row, ch, kt) issues the global load of 16-byte chunk `ch` (0..7) of tile
+// row `row` for K tile `kt`; finish(raw) turns what arrived into the chunk that
+// is written to LDS. Splitting the two lets loads for later K tiles stay in
+// flight while earlier ones are consumed. Rows past the operand's end are
+// clamped to its last row: their products only reach output rows/columns that
+// are never stored.
+
+struct RowLoader {          // plain row-major, K-contiguous operand
+  typedef u32x4 Raw;
+  const char* base;         // first row of this work-group's tile
+  int64_t row_bytes;
+  int rows_valid;           // >= 1
+  __device__ __forceinline__ Raw fetch(int row, int ch, int kt) const {
+    const int r = row < rows_valid ? row : rows_valid - 1;
+    return *reinterpret_cast<const u32x4*>(base + (int64_t)r * row_bytes + kt * kTileKBytes +
+                                           ch * 16);
+  }
+  __device__ __forceinline__ u32x4 finish(const Raw& v) const { return v; }
+};
+
+// A operand of the core GEMM: A[t, r*r3 + s] = c[t, r] * z[t, s], rounded to the
+// operand type. A K tile never straddles two r blocks (r3 is a multiple of the
+// tile's element count).
+template <class Elt>
+struct KhatriRaoLoader {
+  struct Raw {
+    u32x4 v;
+    float c;
+  };
+  const char* z;            // first row of the tile, (., r3)
+  const float* c;           // first row of the tile, (., r1)
+  int r1, r3;
+  int rows_valid;
+  __device__ __forceinline__ Raw fetch(int row, int ch, int kt) const {
+    constexpr int kTileK = kTileKBytes / (int)sizeof(typename Elt::T);
+    const int r = row < rows_valid ? row : rows_valid - 1;
+    const int k0 = kt * kTileK;
+    const int rr = k0 / r3;
+    const int s0 = k0 - rr * r3;
+    Raw o;
+    o.v = *reinterpret_cast<const u32x4*>(
+        z + ((int64_t)r * r3 + s0) * (int64_t)sizeof(typename Elt::T) + ch * 16);
+    o.c = c[(int64_t)r * r1 + rr];
+    return o;
+  }
+  __device__ __forceinline__ u32x4 finish(const Raw& raw) const {
+    u32x4 o;
+    if constexpr (sizeof(typename Elt::T) == 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16x2(bf16_bits_to_f32(raw.v[j] & 0xffffu) * raw.c,
+                           bf16_bits_to_f32(raw.v[j] >> 16) * raw.c);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = __float_as_uint(__uint_as_float(raw.v[j]) * raw.c);
+    }
+    return o;
+  }
+};
+
+// ---- the shared GEMM main loop -------------------------------------------
+// C tile (BM x BN) of A (M x K) * B^T (N x K)^T, fp32 accumulate, 64*WM*WN threads.
+// Waves form a WM x WN grid; wave (wm, wn) owns rows wm*BM/WM.. and columns
+// wn*BN/WN.. of the tile as FM x FN blocks of 32 x 32. BX further B rows are staged
+// with the tile for an `extra` consumer (the router columns of k_front).
+//
+// LDS holds two stages of [BM + BN + BX rows][8 chunks of 16 B]; chunk ch of row
+// r sits at slot ch ^ (r & 7), so the rows one fragment read touches spread
+// over all banks. Global loads run ahead in register rings, PFA K tiles for the
+// A operand and PFB for B: the operand streamed from HBM gets a deep ring (its
+// per-thread share of a tile is small), the L2-resident one a shallow ring. One
+// barrier per K tile.
+template <int BM_, int BN_, int BX_, int WM_, int WN_, int PFA_, int PFB_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, BX = BX_, WM = WM_, WN = WN_;
+  static constexpr int PFA = PFA_, PFB = PFB_;
+  static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
+  static constexpr int FM = kWaveM / 32, FN = kWaveN / 32;
+  static constexpr int kChunks = kTileKBytes / 16;   // 8 per row
+  static constexpr int kBRows = BN + BX;
+  // chunks each thread moves per K tile (the last round may be partial)
+  static constexpr int kAPerThread = (BM * kChunks + kThreads - 1) / kThreads;
+  static constexpr int kBPerThread = (kBRows * kChunks + kThreads - 1) / kThreads;
+  static constexpr int kStage = (BM + kBRows) * kChunks;  // u32x4 slots per stage
+  static constexpr int kLdsBytes = 2 * kStage * 16;
+  static_assert(BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile/wave mismatch");
+  static_assert(PFA >= 1 && PFA <= 8 && PFB >= 1 && PFA % PFB == 0, "prefetch rings");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+};
+
+__device__ __forceinline__ int lds_slot(int row, int ch) { return row * 8 + (ch ^ (row & 7)); }
+
+struct NoExtra {
+  template <class AF>
+  __device__ __forceinline__ void operator()(const u32x4*, int, int, const AF&) const {}
+};
+
+template <class TL, class Elt, class ALoad, class BLoad, class Extra>
+__device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], const ALoad& aload,
+                                              const BLoad& bload, int nkt, u32x4* smem,
+                                              Extra& extra) {
+  constexpr int FM = TL::FM, FN = TL::FN, CH = TL::kChunks;
+  constexpr int PFA = TL::PFA, PFB = TL::PFB;
+  constexpr int kKSteps = kTileKBytes / 32;   // MFMA K steps per K tile
+  constexpr int AP = TL::kAPerThread, BP = TL::kBPerThread;
+  constexpr int kARows = TL::BM, kBRows = TL::kBRows;
+  // the next tile's LDS stores are spread over the last kStashSteps K steps of
+  // the current tile, after each step's MFMAs are issued
+  constexpr int kStashSteps = 2;
+  constexpr int kPerStep = (AP + BP + kStashSteps - 1) / kStashSteps;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = zero16();
+
+  // Tile t is staged in A ring slot t % PFA and B ring slot t % PFB, then in
+  // LDS stage t & 1.
+  typename ALoad::Raw ra[PFA][AP];
+  typename BLoad::Raw rb[PFB][BP];
+
+  auto fetch_a = [&](int kt, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < AP; ++i) {
+      const int q = tid + i * TL::kThreads;
+      if (AP * TL::kThreads == kARows * CH || q < kARows * CH)
+        ra[slot][i] = aload.fetch(q / CH, q % CH, kt);
+    }
+  };
+  auto fetch_b = [&](int kt, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const int q = tid + i * TL::kThreads;
+      if (BP * TL::kThreads == kBRows * CH || q < kBRows * CH)
+        rb[slot][i] = bload.fetch(q / CH, q % CH, kt);
+    }
+  };
+  // chunk index c < AP + BP: A chunks first, then B chunks
+  auto stash_chunk = [&](int c, int sa, int sb, u32x4* s) __attribute__((always_inline)) {
+    if (c < AP) {
+      const int q = tid + c * TL::kThreads;
+      if (AP * TL::kThreads == kARows * CH || q < kARows * CH)
+        s[lds_slot(q / CH, q % CH)] = aload.finish(ra[sa][c]);
+    } else if (c < AP + BP) {
+      const int q = tid + (c - AP) * TL::kThreads;
+      if (BP * TL::kThreads == kBRows * CH || q < kBRows * CH)
+        s[lds_slot(kARows + q / CH, q % CH)] = bload.finish(rb[sb][c - AP]);
+    }
+  };
+  // MFMAs of tile kt from LDS stage kt & 1; with `stash`, ring slots (sa, sb)
+  // (tile kt + 1) are written to the other stage in between.
+  auto compute = [&](int kt, bool stash, int sa, int sb) __attribute__((always_inline)) {
+    const u32x4* s = smem + (kt & 1) * TL::kStage;
+    u32x4* so = smem + ((kt + 1) & 1) * TL::kStage;
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) {
+      const int ch = ks * 2 + (lane >> 5);
+      u32x4 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = s[lds_slot(wm * TL::kWaveM + i * 32 + (lane & 31), ch)];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = s[lds_slot(kARows + wn * TL::kWaveN + j * 32 + (lane & 31), ch)];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], af[i], bfr[j], Elt{});
+      extra(s, kt * kKSteps + ks, ch, af);
+      if (stash && ks >= kKSteps - kStashSteps) {
+        const int c0 = (ks - (kKSteps - kStashSteps)) * kPerStep;
+#pragma unroll
+        for (int c = 0; c < kPerStep; ++c) stash_chunk(c0 + c, sa, sb, so);
+      }
+    }
+  };
+
+  // prologue: tile 0 into LDS stage 0, then tiles 1 .. PFA (A) and 1 .. PFB (B)
+  // in flight
+  fetch_a(0, 0);
+  fetch_b(0, 0);
+#pragma unroll
+  for (int c = 0; c < AP + BP; ++c) stash_chunk(c, 0, 0, smem);
+#pragma unroll
+  for (int p = 1; p <= PFA; ++p)
+    if (p < nkt) fetch_a(p, p % PFA);
+#pragma unroll
+  for (int p = 1; p <= PFB; ++p)
+    if (p < nkt) fetch_b(p, p % PFB);
+  __syncthreads();
+
+  for (int k0 = 0; k0 < nkt; k0 += PFA) {
+#pragma unroll
+    for (int p = 0; p < PFA; ++p) {
+      const int kt = k0 + p;
+      if (kt < nkt) {
+        // ring slots of tile kt + 1 (k0 is a multiple of PFA, hence of PFB)
+        const int sa = (p + 1) % PFA, sb = (p + 1) % PFB;
+        // stage (kt + 1) & 1 was last read while computing tile kt - 1, which
+        // every wave finished before the previous barrier
+        compute(kt, kt + 1 < nkt, sa, sb);
+        if (kt + 1 + PFA < nkt) fetch_a(kt + 1 + PFA, sa);
+        if (kt + 1 + PFB < nkt) fetch_b(kt + 1 + PFB, sb);
+        __syncthreads();
+      }
+    }
+  }
+}
+
+// Work-group -> tile order for 2-D grids launched as 1-D. Consecutive
+// work-groups land on different XCDs (round robin over 8); this hands each XCD a
+// contiguous run of tiles, row-major over (m, n), so the A rows of an m tile are
+// fetched into one XCD's L2 and reused for all its n tiles.
+__device__ __forceinline__ void tile_coords(int n_tiles_n, int n_tiles, int& tm, int& tn) {
+  const int b = blockIdx.x;
+  const int per = n_tiles / 8;
+  const int t = b < per * 8 ? (b % 8) * per + b / 8 : b;
+  tm = t / n_tiles_n;
+  tn = t - tm * n_tiles_n;
+}
+
+// ---- C tile store through LDS ----------------------------------------------
+// The MFMA result layout gives each lane one column of sixteen rows, so direct
+// stores would be 2- or 4-byte scatters. The tile is instead converted into LDS
+// (rows padded by 16 bytes, which puts the two row groups one store instruction
+// touches on distinct banks) and written out as 16-byte, row-contiguous chunks.
+template <class TL, class T>
+struct TileStage {
+  static constexpr int kRowBytes = TL::BN * (int)sizeof(T) + 16;
+  static constexpr int kBytes = TL::BM * kRowBytes;
+};
+
+// Stores acc + colv[j] (colv: a per-column addend this lane holds for each of its
+// FN column blocks, loaded once before the loop) as T.
+template <class TL, class T>
+__device__ __forceinline__ void stage_tile(const f32x16 (&acc)[TL::FM][TL::FN], char* stage,
+                                           const float (&colv)[TL::FN]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
+  constexpr int RB = TileStage<TL, T>::kRowBytes;
+#pragma unroll
+  for (int j = 0; j < TL::FN; ++j) {
+    const int col = wn * TL::kWaveN + j * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < TL::FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * TL::kWaveM + i * 32 + acc_row(lane, e);
+        store_from_f32(reinterpret_cast<T*>(stage + row * RB + col * (int)sizeof(T)),
+                       acc[i][j][e] + colv[j]);
+      }
+  }
+}
+
+// Copies a staged tile to dst (the tile's origin, leading dimension ld
+// elements). Columns are only ever cut at multiples of 16, so a 16-byte chunk is
+// wholly inside or wholly outside the valid columns. The stores are streaming
+// (nontemporal): the tile is not read again by this kernel, and allocating it in
+// L2 would evict the operand tiles the next work-groups read.
+template <class TL, class T>
+__device__ __forceinline__ void flush_tile(const char* stage, T* dst, int64_t ld, int rows_valid,
+                                           int cols_valid) {
+  constexpr int RB = TileStage<TL, T>::kRowBytes;
+  constexpr int CPR = TL::BN * (int)sizeof(T) / 16;   // chunks per row
+  constexpr int EPC = 16 / (int)sizeof(T);           // elements per chunk
+  for (int c = threadIdx.x; c < TL::BM * CPR; c += TL::kThreads) {
+    const int row = c / CPR, ch = c - row * CPR;
+    if (row < rows_valid && ch * EPC < cols_valid)
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + row * RB + ch * 16),
+                                  reinterpret_cast<u32x4*>(dst + row * ld + ch * EPC));
+  }
+}
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+// ---- k_front: in-projection + RMSNorm, router + top-k + softmax + c --------
+// model.py:75-81 (+ the U_expert gather of :93 folded into c). One work-group:
+// 64 tokens x (R3 z columns + EP router columns), NW = R3 / 32 (at most 4) waves
+// side by side over the z columns, each owning all 64 rows.
+//  z part: epilogue z = (z / rms) * g with rms = sqrt(mean(z^2) + eps)
+//  (model.py:25-27), the division taken as a multiply by 1 / rms.
+//  router part (NR = EP/32 column blocks): with NR < NW every wave computes all
+//  router columns over every NW-th K step and the partial sums are added in
+//  wave order; otherwise the waves split the router columns. Top-k: k rounds
+//  of a wave-wide arg-max over the row's logits: larger logit first, NaN above
+//  every number (torch.topk's order), equal values by lower expert index.
+__device__ __forceinline__ bool ranks_before(float v1, int i1, float v2, int i2) {
+  if (i2 == 0x7fffffff) return i1 != 0x7fffffff;
+  if (i1 == 0x7fffffff) return false;
+  const bool n1 = v1 != v1, n2 = v2 != v2;
+  if (n1 || n2) return n1 && (!n2 || i1 < i2);
+  return v1 > v2 || (v1 == v2 && i1 < i2);
+}
+
+template <class Elt, int FM, int NR, int NW>
+struct RouterExtra {
+  static constexpr bool kSplitK = NR < NW;
+  static constexpr int RT = kSplitK ? NR : NR / NW;   // router column blocks per wave
+  static_assert(kSplitK || NR % NW == 0, "router split");
+  f32x16 racc[FM][RT];
+  int wave, lane, brow0;   // brow0: LDS row of router column 0
+  __device__ __forceinline__ void init(int w, int l, int r0) {
+    wave = w;
+    lane = l;
+    brow0 = r0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < RT; ++j) racc[i][j] = zero16();
+  }
+  template <class AF>
+  __device__ __forceinline__ void operator()(const u32x4* s, int kstep, int ch, const AF& af) {
+    if (kSplitK && (kstep % NW) != wave) return;
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int col0 = (kSplitK ? j : wave * RT + j) * 32;
+      const u32x4 b = s[lds_slot(brow0 + col0 + (lane & 31), ch)];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) mma(racc[i][j], af[i], b, Elt{});
+    }
+  }
+};
+
+template <class Elt, int R3, int NR, int PFA = kFrontPFA>
+__global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
+  typedef typename Elt::T T;
+  constexpr int BM = kFrontBM, EP = 32 * NR;
+  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
+  // x streams from HBM once: its ring holds PFA tiles (2 chunks per thread
+  // each). The weight rows come from L2: one tile ahead, or two when a thread's
+  // share is small enough that two sets do not spill.
+  constexpr int kBChunks = (R3 + EP) * 8 / (64 * NW);
+  typedef Tile<BM, R3, EP, 1, NW, PFA, (kBChunks > 10 || PFA % 2 != 0 ? 1 : 2)> TL;
+  constexpr int FM = TL::FM;   // 2: all 64 rows
+  typedef RouterExtra<Elt, FM, NR, NW> RX;
+  // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
+  constexpr int LD = EP + 1;
+  constexpr int kPlanes = RX::kSplitK ? NW : 1;
+  constexpr int kZBytes = TileStage<TL, T>::kBytes;
+  constexpr int kEpiBytes = kZBytes + (kPlanes * BM * LD + NW * BM) * 4;
+  // U_expert is staged after that: at least 4 KB (E = 256, r1 = 4) of room
+  constexpr int kSmemBytes = cmax(TL::kLdsBytes, kEpiBytes + 4096);
+  __shared__ u32x4 smem[kSmemBytes / 16];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m0 = (int64_t)blockIdx.x * BM;
+  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+  const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
+  RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes, row_bytes, rows_valid};
+  RowLoader bl{reinterpret_cast<const char*>(a.wfront), row_bytes, R3 + EP};
+  f32x16 acc[FM][TL::FN];
+  RX rx;
+  rx.init(wave, lane, BM + R3);
+  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, rx);
+
+  // -- router logits -> LDS, [BM][EP + 1] (split-K: one partial plane per wave) --
+  char* zst = reinterpret_cast<char*>(smem);
+  float* lg = reinterpret_cast<float*>(zst + kZBytes);
+  float* red = lg + kPlanes * BM * LD;   // [NW][BM] RMSNorm partial sums
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < RX::RT; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = i * 32 + acc_row(lane, e);
+        if constexpr (RX::kSplitK)
+          lg[(wave * BM + row) * LD + j * 32 + (lane & 31)] = rx.racc[i][j][e];
+        else
+          lg[row * LD + (wave * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
+      }
+
+  // -- RMSNorm row sums of squares ------------------------------------------
+  // lanes l and l ^ m (m < 32) hold the same rows
+  float ss[FM][16];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < TL::FN; ++j) v += acc[i][j][e] * acc[i][j][e];
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off);
+      ss[i][e] = v;
+    }
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) red[wave * BM + i * 32 + acc_row(lane, e)] = ss[i][e];
+  }
+  __syncthreads();
+
+  // -- z = (z / rms) * g, staged in LDS then written as 16-byte chunks ----------
+  {
+    constexpr int RB = TileStage<TL, T>::kRowBytes;
+    float gcol[TL::FN];
+#pragma unroll
+    for (int j = 0; j < TL::FN; ++j) gcol[j] = a.gain[wave * TL::kWaveN + j * 32 + (lane & 31)];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = i * 32 + acc_row(lane, e);
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot += red[w * BM + row];
+        // z / rms as z * (1 / rms): within one fp32 rounding of the division
+        const float inv_rms = 1.f / sqrtf(tot / (float)R3 + a.eps);
+#pragma unroll
+        for (int j = 0; j < TL::FN; ++j) {
+          const int col = wave * TL::kWaveN + j * 32 + (lane & 31);
+          store_from_f32(reinterpret_cast<T*>(zst + row * RB + col * (int)sizeof(T)),
+                         (acc[i][j][e] * inv_rms) * gcol[j]);
+        }
+      }
+  }
+  __syncthreads();
+  flush_tile<TL, T>(zst, reinterpret_cast<T*>(a.z) + m0 * R3, R3, rows_valid, R3);
+
+  // -- top-k, softmax, c -------------------------------------------------------
+  // Each row is resolved by a group of G lanes holding 4 logits each (columns
+  // gl, gl + G, ...), so a wave works on 64 / G rows at once. U_expert is read
+  // from LDS when it fits in the space left after the logits.
+  constexpr int G = EP / 4 < 8 ? 8 : (EP / 4 > 64 ? 64 : EP / 4);
+  constexpr int PL = EP / G;          // logits per lane
+  constexpr int RPW = 64 / G;         // rows per wave per pass
+  constexpr int kUeBytes = kSmemBytes - kEpiBytes;
+  const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
+  const bool ue_lds = E * R1 * 4 <= kUeBytes;
+  float* ue = red + NW * BM;
+  if (ue_lds)
+    for (int i = threadIdx.x; i < E * R1; i += TL::kThreads) ue[i] = a.uexp[i];
+  __syncthreads();
+  const float* uex = ue_lds ? ue : a.uexp;
+  const int gl = lane % G;
+  for (int row0 = wave * RPW; row0 < BM; row0 += NW * RPW) {
+    const int row = row0 + lane / G;
+    const bool live = row < rows_valid;
+    const int64_t g = m0 + row;
+    float v[PL];
+    unsigned taken = 0;
+#pragma unroll
+    for (int p = 0; p < PL; ++p) {
+      const int col = gl + G * p;
+      float sc = 0.f;
+      if constexpr (RX::kSplitK) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sc += lg[(w * BM + row) * LD + col];
+      } else {
+        sc = lg[row * LD + col];
+      }
+      v[p] = sc;
+      if (a.logits && live && col < E) a.logits[g * E + col] = sc;
+    }
+    float sel_v[kMaxTopK];
+    int sel_i[kMaxTopK];
+#pragma unroll
+    for (int kk = 0; kk < kMaxTopK; ++kk) {
+      sel_v[kk] = 0.f;
+      sel_i[kk] = 0;
+      if (kk < K) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;   // "no candidate": loses to every real one
+#pragma unroll
+        for (int p = 0; p < PL; ++p) {
+          const int col = gl + G * p;
+          const bool ok = col < E && !((taken >> p) & 1u);
+          if (ok && ranks_before(v[p], col, bv, bi)) {
+            bv = v[p];
+            bi = col;
+          }
+        }
+#pragma unroll
+        for (int off = G / 2; off >= 1; off >>= 1) {   // stays inside the group
+          const float ov = __shfl_xor(bv, off);
+          const int oi = __shfl_xor(bi, off);
+          if (ranks_before(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        // k <= E, so a candidate always remains and bi < E here.
+        if (bi % G == gl) taken |= 1u << (bi / G);
+        sel_v[kk] = bv;
+        sel_i[kk] = bi;
+      }
+    }
+    // softmax over the selected logits (sel_v[0] is the largest)
+    float ex[kMaxTopK];
+    float ssum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < kMaxTopK; ++kk) {
+      ex[kk] = 0.f;
+      if (kk < K) {
+        ex[kk] = expf(sel_v[kk] - sel_v[0]);
+        ssum += ex[kk];
+      }
+    }
+    if (live) {
+#pragma unroll
+      for (int kk = 0; kk < kMaxTopK; ++kk) {
+        if (kk < K && kk % G == gl) {
+          a.idx[g * K + kk] = sel_i[kk];
+          a.w[g * K + kk] = ex[kk] / ssum;
+        }
+      }
+      // c[r] = sum_j w_j * U_expert[e_j, r]
+      for (int r = gl; r < R1; r += G) {
+        float cr = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < kMaxTopK; ++kk)
+          if (kk < K) cr += (ex[kk] / ssum) * uex[sel_i[kk] * R1 + r];
+        a.c[g * R1 + r] = cr;
+      }
+    }
+  }
+}
+
+// ---- k_core: mid = (c (x) z) core_flat  (model.py:87-98) ------------------
+template <class Elt, int BM, int BN, int WM, int WN, int PFA, int PFB>
+__global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
+  typedef typename Elt::T T;
+  typedef Tile<BM, BN, 0, WM, WN, PFA, PFB> TL;
+  __shared__ u32x4 smem[cmax(TL::kLdsBytes, TileStage<TL, T>::kBytes) / 16];
+
+  const int ntn = (int)((a.r2 + BN - 1) / BN);
+  const int ntm = (int)((a.T + BM - 1) / BM);
+  int tm, tn;
+  tile_coords(ntn, ntm * ntn, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t n0 = (int64_t)tn * BN;
+  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+  const int64_t K = a.r1 * a.r3;
+  const int64_t b_row_bytes = K * (int64_t)sizeof(T);
+  KhatriRaoLoader<Elt> al{reinterpret_cast<const char*>(a.z) + m0 * a.r3 * (int64_t)sizeof(T),
+                          a.c + m0 * a.r1, (int)a.r1, (int)a.r3, rows_valid};
+  RowLoader bl{reinterpret_cast<const char*>(a.coreT) + n0 * b_row_bytes, b_row_bytes,
+               (int)(a.r2 - n0)};
+  f32x16 acc[TL::FM][TL::FN];
+  NoExtra nx;
+  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(b_row_bytes / kTileKBytes), smem, nx);
+
+  char* stage = reinterpret_cast<char*>(smem);
+  float zero[TL::FN];
+#pragma unroll
+  for (int j = 0; j < TL::FN; ++j) zero[j] = 0.f;
+  stage_tile<TL, T>(acc, stage, zero);
+  __syncthreads();
+  flush_tile<TL, T>(stage, reinterpret_cast<T*>(a.mid) + m0 * a.r2 + n0, a.r2, rows_valid,
+                    (int)(a.r2 - n0));
+}
+
+// ---- k_outproj: out = mid U_out + bias  (model.py:101) --------------------
+template <class Elt, int BM, int BN, int WM, int WN, int PFA, int PFB>
+__global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
+  typedef typename Elt::T T;
+  typedef Tile<BM, BN, 0, WM, WN, PFA, PFB> TL;
+  __shared__ u32x4 smem[cmax(TL::kLdsBytes, TileStage<TL, T>::kBytes) / 16];
+
+  const int ntn = (int)((a.d_out + BN - 1) / BN);
+  const int ntm = (int)((a.T + BM - 1) / BM);
+  int tm, tn;
+  tile_coords(ntn, ntm * ntn, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t n0 = (int64_t)tn * BN;
+  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+  const int64_t row_bytes = a.r2 * (int64_t)sizeof(T);
+  RowLoader al{reinterpret_cast<const char*>(a.mid) + m0 * row_bytes, row_bytes, rows_valid};
+  RowLoader bl{reinterpret_cast<const char*>(a.uoutT) + n0 * row_bytes, row_bytes,
+               (int)(a.d_out - n0)};
+  f32x16 acc[TL::FM][TL::FN];
+  NoExtra nx;
+  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, nx);
+
+  char* stage = reinterpret_cast<char*>(smem);
+  const int cols_valid = (int)(a.d_out - n0);
+  float bcol[TL::FN];
+  {
+    const int wn = (threadIdx.x >> 6) % WN, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < TL::FN; ++j) {
+      const int col = wn * TL::kWaveN + j * 32 + (lane & 31);
+      bcol[j] = col < cols_valid ? a.bias[n0 + col] : 0.f;
+    }
+  }
+  stage_tile<TL, T>(acc, stage, bcol);
+  __syncthreads();
+  flush_tile<TL, T>(stage, reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0, a.d_out, rows_valid,
+                    cols_valid);
+}
+
+// ---- packing kernels -----------------------------------------------------
+template <class T>
+__global__ void k_transpose(const T* __restrict__ src, T* __restrict__ dst, int64_t rows,
+                            int64_t cols) {
+  __shared__ T tile[32][33];
+  const int64_t c0 = (int64_t)blockIdx.x * 32, r0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8 threads
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t r = r0 + y, c = c0 + tx;
+    if (r < rows && c < cols) tile[y][tx] = src[r * cols + c];
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t c = c0 + y, r = r0 + tx;   // dst row c, column r
+    if (r < rows && c < cols) dst[c * rows + r] = tile[tx][y];
+  }
+}
+
+template <class T>
+__global__ void k_copy_pad(const T* __restrict__ src, T* __restrict__ dst, int64_t n,
+                           int64_t n_pad) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_pad;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = i < n ? src[i] : T(0);
+}
+
+template <class T>
+__global__ void k_to_f32(const T* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = load_as_f32(src + i);
+}
+
+}  // namespace dev
+}  // namespace tmoe
