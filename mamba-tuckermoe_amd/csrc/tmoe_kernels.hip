@@ -11,13 +11,13 @@ constexpr int kDtypeBF16 = 1;   // TMOE_BF16
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
-// GEMM tiles (BM x BN, WM x WN waves, A/B prefetch rings PFA/PFB) per kernel and
-// dtype. bf16 choices measured at T=16384: core 256x256 tiles are one per CU;
-// out-projection 256x192 tiles make 768 = 3 x 256 work-groups, no partial wave.
-struct CoreCfgBF16 { static constexpr int BM = 256, BN = 256, WM = 2, WN = 4, PFA = 1, PFB = 1; };
-struct OutCfgBF16 { static constexpr int BM = 256, BN = 192, WM = 4, WN = 2, PFA = 2, PFB = 2; };
-struct CoreCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, PFA = 2, PFB = 2; };
-struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, PFA = 2, PFB = 2; };
+// GEMM tiles per kernel and dtype: BM x BN, WM x WN waves; core: register ring
+// depth PFA of the c (x) z operand; out-projection: LDS stages NS. bf16 choices
+// measured at T=16384.
+struct CoreCfgBF16 { static constexpr int BM = 256, BN = 256, WM = 2, WN = 4, P = 1; };
+struct OutCfgBF16 { static constexpr int BM = 256, BN = 192, WM = 4, WN = 2, P = 2; };
+struct CoreCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 2; };
+struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 2; };
 
 template <class Elt, int R3>
 hipError_t launch_front_r3(const FwdArgs& a, hipStream_t st) {
@@ -46,16 +46,15 @@ hipError_t launch_front_t(const FwdArgs& a, hipStream_t st) {
 template <class Elt, class C>
 hipError_t launch_core_t(const FwdArgs& a, hipStream_t st) {
   const dim3 grid(cdiv(a.T, C::BM) * cdiv(a.r2, C::BN)), block(64 * C::WM * C::WN);
-  hipLaunchKernelGGL((dev::k_core<Elt, C::BM, C::BN, C::WM, C::WN, C::PFA, C::PFB>), grid, block,
-                     0, st, a);
+  hipLaunchKernelGGL((dev::k_core<Elt, C::BM, C::BN, C::WM, C::WN, C::P>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
 template <class Elt, class C>
 hipError_t launch_outproj_t(const FwdArgs& a, hipStream_t st) {
   const dim3 grid(cdiv(a.T, C::BM) * cdiv(a.d_out, C::BN)), block(64 * C::WM * C::WN);
-  hipLaunchKernelGGL((dev::k_outproj<Elt, C::BM, C::BN, C::WM, C::WN, C::PFA, C::PFB>), grid,
-                     block, 0, st, a);
+  hipLaunchKernelGGL((dev::k_outproj<Elt, C::BM, C::BN, C::WM, C::WN, C::P>), grid, block, 0, st,
+                     a);
   return hipGetLastError();
 }
 

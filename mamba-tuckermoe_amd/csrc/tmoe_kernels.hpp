@@ -92,13 +92,16 @@ __device__ __forceinline__ f32x16 zero16() {
 
 struct RowLoader {          // plain row-major, K-contiguous operand
   typedef u32x4 Raw;
+  static constexpr int kVmem = 1;   // vector memory instructions per fetch
   const char* base;         // first row of this work-group's tile
   int64_t row_bytes;
   int rows_valid;           // >= 1
-  __device__ __forceinline__ Raw fetch(int row, int ch, int kt) const {
+  __device__ __forceinline__ const char* gaddr(int row, int ch, int kt) const {
     const int r = row < rows_valid ? row : rows_valid - 1;
-    return *reinterpret_cast<const u32x4*>(base + (int64_t)r * row_bytes + kt * kTileKBytes +
-                                           ch * 16);
+    return base + (int64_t)r * row_bytes + kt * kTileKBytes + ch * 16;
+  }
+  __device__ __forceinline__ Raw fetch(int row, int ch, int kt) const {
+    return *reinterpret_cast<const u32x4*>(gaddr(row, ch, kt));
   }
   __device__ __forceinline__ u32x4 finish(const Raw& v) const { return v; }
 };
@@ -112,6 +115,7 @@ struct KhatriRaoLoader {
     u32x4 v;
     float c;
   };
+  static constexpr int kVmem = 2;   // z chunk + c scalar
   const char* z;            // first row of the tile, (., r3)
   const float* c;           // first row of the tile, (., r1)
   int r1, r3;
@@ -146,33 +150,62 @@ struct KhatriRaoLoader {
 // ---- the shared GEMM main loop -------------------------------------------
 // C tile (BM x BN) of A (M x K) * B^T (N x K)^T, fp32 accumulate, 64*WM*WN threads.
 // Waves form a WM x WN grid; wave (wm, wn) owns rows wm*BM/WM.. and columns
-// wn*BN/WN.. of the tile as FM x FN blocks of 32 x 32. BX further B rows are staged
-// with the tile for an `extra` consumer (the router columns of k_front).
+// wn*BN/WN.. of the tile as FM x FN blocks of 32 x 32. BX further B rows are
+// staged with the tile for an `extra` consumer (the router columns of k_front).
 //
-// LDS holds two stages of [BM + BN + BX rows][8 chunks of 16 B]; chunk ch of row
-// r sits at slot ch ^ (r & 7), so the rows one fragment read touches spread
-// over all banks. Global loads run ahead in register rings, PFA K tiles for the
-// A operand and PFB for B: the operand streamed from HBM gets a deep ring (its
-// per-thread share of a tile is small), the L2-resident one a shallow ring. One
-// barrier per K tile.
-template <int BM_, int BN_, int BX_, int WM_, int WN_, int PFA_, int PFB_>
+// LDS holds NS stages of [BM + BN + BX rows][8 chunks of 16 B]; chunk ch of row
+// r sits at slot ch ^ (r & 7), so the rows one fragment read touches spread over
+// all banks. Each operand reaches LDS one of two ways:
+//  * DMA (ADMA / BDMA): global_load_lds_dwordx4 writes LDS directly; one wave
+//    instruction fills one 1 KB block of 8 rows, lane l fetching logical chunk
+//    (l & 7) ^ (l >> 3) so the swizzle is kept. Tile kt + NS - 1 is issued
+//    while tile kt is computed.
+//  * a register ring of PFA / PFB tiles (for an operand that is transformed on
+//    the way, or streamed from HBM and wanting more tiles in flight); tile kt+1
+//    is written to LDS in between the MFMAs of tile kt.
+// One barrier per K tile, preceded by an explicit wait for exactly the loads
+// tile kt + 1 needs (the compiler's own barrier would wait for every load).
+template <int BM_, int BN_, int BX_, int WM_, int WN_, int PFA_, int PFB_, int NS_ = 2,
+          bool ADMA_ = false, bool BDMA_ = false>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, BX = BX_, WM = WM_, WN = WN_;
-  static constexpr int PFA = PFA_, PFB = PFB_;
+  static constexpr int PFA = PFA_, PFB = PFB_, NS = NS_;
+  static constexpr bool ADMA = ADMA_, BDMA = BDMA_;
   static constexpr int kThreads = 64 * WM * WN;
   static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
   static constexpr int FM = kWaveM / 32, FN = kWaveN / 32;
   static constexpr int kChunks = kTileKBytes / 16;   // 8 per row
   static constexpr int kBRows = BN + BX;
-  // chunks each thread moves per K tile (the last round may be partial)
+  // register-staged chunks each thread moves per K tile
   static constexpr int kAPerThread = (BM * kChunks + kThreads - 1) / kThreads;
   static constexpr int kBPerThread = (kBRows * kChunks + kThreads - 1) / kThreads;
   static constexpr int kStage = (BM + kBRows) * kChunks;  // u32x4 slots per stage
-  static constexpr int kLdsBytes = 2 * kStage * 16;
+  static constexpr int kLdsBytes = NS * kStage * 16;
   static_assert(BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile/wave mismatch");
   static_assert(PFA >= 1 && PFA <= 8 && PFB >= 1 && PFA % PFB == 0, "prefetch rings");
+  static_assert(NS >= 2 && NS <= 4, "LDS stages");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef const __attribute__((address_space(1))) void* gbl_cvptr;
+
+// s_waitcnt with vmcnt <= VM and lgkmcnt == 0 (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int VM>
+__device__ __forceinline__ void wait_vm_lds() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
+}
+
+// Work-group barrier that orders LDS traffic only; loads still in flight stay in
+// flight. The empty asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ int lds_slot(int row, int ch) { return row * 8 + (ch ^ (row & 7)); }
 
@@ -185,15 +218,33 @@ template <class TL, class Elt, class ALoad, class BLoad, class Extra>
 __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], const ALoad& aload,
                                               const BLoad& bload, int nkt, u32x4* smem,
                                               Extra& extra) {
-  constexpr int FM = TL::FM, FN = TL::FN, CH = TL::kChunks;
-  constexpr int PFA = TL::PFA, PFB = TL::PFB;
+  constexpr int FM = TL::FM, FN = TL::FN, CH = TL::kChunks, NS = TL::NS;
+  constexpr bool ADMA = TL::ADMA, BDMA = TL::BDMA;
+  constexpr int PFA = ADMA ? 1 : TL::PFA, PFB = BDMA ? 1 : TL::PFB;
   constexpr int kKSteps = kTileKBytes / 32;   // MFMA K steps per K tile
-  constexpr int AP = TL::kAPerThread, BP = TL::kBPerThread;
+  constexpr int W = TL::kThreads / 64;
   constexpr int kARows = TL::BM, kBRows = TL::kBRows;
-  // the next tile's LDS stores are spread over the last kStashSteps K steps of
-  // the current tile, after each step's MFMAs are issued
+  constexpr int AP = ADMA ? 0 : TL::kAPerThread, BP = BDMA ? 0 : TL::kBPerThread;
+  // DMA instructions each wave issues per tile
+  constexpr int ADN = ADMA ? kARows / 8 / W : 0, BDN = BDMA ? kBRows / 8 / W : 0;
+  static_assert(!ADMA || (kARows / 8) % W == 0, "A DMA blocks must split evenly over waves");
+  static_assert(!BDMA || (kBRows / 8) % W == 0, "B DMA blocks must split evenly over waves");
+  // every thread issues the same loads, so one vmcnt count holds for all waves
+  static_assert(ADMA || AP * TL::kThreads == kARows * CH, "register-staged A: full rounds");
+  static_assert(BDMA || BP * TL::kThreads == kBRows * CH, "register-staged B: full rounds");
+  // vector memory instructions per tile: register rings (per fetch) and DMA
+  constexpr int FA = AP * ALoad::kVmem, FB = BP * BLoad::kVmem, D = ADN + BDN;
+  // loads issued after tile kt+1's DMA until the end of iteration kt (steady state)
+  constexpr int kVmAfter = (NS - 2) * D + (NS - 1) * (FA + FB);
+  // Memory instructions are spread over the K steps of a tile, each after that
+  // step's MFMAs, so a wave never stalls on a full memory queue with MFMAs left
+  // to issue: DMA of tile kt + NS - 1 over the first kDmaSteps steps; the
+  // register-staged LDS stores of tile kt + 1 and the ring refills that reuse
+  // their registers over the last kStashSteps steps.
   constexpr int kStashSteps = 2;
+  constexpr int kDmaSteps = AP + BP > 0 ? kKSteps - kStashSteps : kKSteps;
   constexpr int kPerStep = (AP + BP + kStashSteps - 1) / kStashSteps;
+  constexpr int kDmaPerStep = (ADN + BDN + kDmaSteps - 1) / kDmaSteps;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -204,44 +255,76 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = zero16();
 
-  // Tile t is staged in A ring slot t % PFA and B ring slot t % PFB, then in
-  // LDS stage t & 1.
-  typename ALoad::Raw ra[PFA][AP];
-  typename BLoad::Raw rb[PFB][BP];
+  // Register rings: tile t in A slot t % PFA and B slot t % PFB.
+  typename ALoad::Raw ra[PFA][AP > 0 ? AP : 1];
+  typename BLoad::Raw rb[PFB][BP > 0 ? BP : 1];
 
   auto fetch_a = [&](int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < AP; ++i) {
       const int q = tid + i * TL::kThreads;
-      if (AP * TL::kThreads == kARows * CH || q < kARows * CH)
-        ra[slot][i] = aload.fetch(q / CH, q % CH, kt);
+      ra[slot][i] = aload.fetch(q / CH, q % CH, kt);
     }
   };
   auto fetch_b = [&](int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
       const int q = tid + i * TL::kThreads;
-      if (BP * TL::kThreads == kBRows * CH || q < kBRows * CH)
-        rb[slot][i] = bload.fetch(q / CH, q % CH, kt);
+      rb[slot][i] = bload.fetch(q / CH, q % CH, kt);
     }
   };
-  // chunk index c < AP + BP: A chunks first, then B chunks
+  // DMA instruction j < ADN + BDN of tile kt into LDS stage `stage` (A blocks
+  // first, then B blocks)
+  auto dma_one = [&](int j, int kt, int stage) __attribute__((always_inline)) {
+    u32x4* s = smem + stage * TL::kStage;
+    const int lc = (lane & 7) ^ (lane >> 3);
+    if (j < ADN) {
+      if constexpr (ADMA) {
+        const int blk = wave + j * W;
+        __builtin_amdgcn_global_load_lds((gbl_cvptr)aload.gaddr(blk * 8 + (lane >> 3), lc, kt),
+                                         (lds_vptr)(s + blk * 64), 16, 0, 0);
+      }
+    } else if (j < ADN + BDN) {
+      if constexpr (BDMA) {
+        const int blk = wave + (j - ADN) * W;
+        __builtin_amdgcn_global_load_lds((gbl_cvptr)bload.gaddr(blk * 8 + (lane >> 3), lc, kt),
+                                         (lds_vptr)(s + (kARows + blk * 8) * 8), 16, 0, 0);
+      }
+    }
+  };
+  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < ADN + BDN; ++j) dma_one(j, kt, stage);
+  };
+  // ring refill of register-staged chunk c for tile kt (A slot sa / B slot sb)
+  auto refill_chunk = [&](int c, int kt, int sa, int sb) __attribute__((always_inline)) {
+    if (c < AP) {
+      const int q = tid + c * TL::kThreads;
+      ra[sa][c] = aload.fetch(q / CH, q % CH, kt);
+    } else if (c < AP + BP) {
+      const int q = tid + (c - AP) * TL::kThreads;
+      rb[sb][c - AP] = bload.fetch(q / CH, q % CH, kt);
+    }
+  };
+  // register-staged chunk c < AP + BP: A chunks first, then B chunks
   auto stash_chunk = [&](int c, int sa, int sb, u32x4* s) __attribute__((always_inline)) {
     if (c < AP) {
       const int q = tid + c * TL::kThreads;
-      if (AP * TL::kThreads == kARows * CH || q < kARows * CH)
-        s[lds_slot(q / CH, q % CH)] = aload.finish(ra[sa][c]);
+      s[lds_slot(q / CH, q % CH)] = aload.finish(ra[sa][c]);
     } else if (c < AP + BP) {
       const int q = tid + (c - AP) * TL::kThreads;
-      if (BP * TL::kThreads == kBRows * CH || q < kBRows * CH)
-        s[lds_slot(kARows + q / CH, q % CH)] = bload.finish(rb[sb][c - AP]);
+      s[lds_slot(kARows + q / CH, q % CH)] = bload.finish(rb[sb][c - AP]);
     }
   };
-  // MFMAs of tile kt from LDS stage kt & 1; with `stash`, ring slots (sa, sb)
-  // (tile kt + 1) are written to the other stage in between.
-  auto compute = [&](int kt, bool stash, int sa, int sb) __attribute__((always_inline)) {
-    const u32x4* s = smem + (kt & 1) * TL::kStage;
-    u32x4* so = smem + ((kt + 1) & 1) * TL::kStage;
+  // MFMAs of tile kt, with the memory work of this iteration in between: DMA of
+  // tile kt + NS - 1; stores of ring slots (sa, sb) (tile kt + 1) to that tile's
+  // stage and their refill with tiles kt + 1 + PFA / kt + 1 + PFB.
+  auto compute = [&](int kt, int sa, int sb) __attribute__((always_inline)) {
+    const bool stash = kt + 1 < nkt;
+    const bool do_dma = kt + NS - 1 < nkt;
+    const bool refill_a = kt + 1 + PFA < nkt, refill_b = kt + 1 + PFB < nkt;
+    const u32x4* s = smem + (kt % NS) * TL::kStage;
+    u32x4* so = smem + ((kt + 1) % NS) * TL::kStage;
 #pragma unroll
     for (int ks = 0; ks < kKSteps; ++ks) {
       const int ch = ks * 2 + (lane >> 5);
@@ -256,27 +339,45 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
 #pragma unroll
         for (int j = 0; j < FN; ++j) mma(acc[i][j], af[i], bfr[j], Elt{});
       extra(s, kt * kKSteps + ks, ch, af);
-      if (stash && ks >= kKSteps - kStashSteps) {
+      if (ADN + BDN > 0 && do_dma && ks < kDmaSteps) {
+#pragma unroll
+        for (int j = 0; j < kDmaPerStep; ++j) dma_one(ks * kDmaPerStep + j, kt + NS - 1, (kt + NS - 1) % NS);
+      }
+      if (AP + BP > 0 && stash && ks >= kKSteps - kStashSteps) {
         const int c0 = (ks - (kKSteps - kStashSteps)) * kPerStep;
 #pragma unroll
         for (int c = 0; c < kPerStep; ++c) stash_chunk(c0 + c, sa, sb, so);
+#pragma unroll
+        for (int c = 0; c < kPerStep; ++c) {
+          const int cc = c0 + c;
+          if (cc < AP ? refill_a : refill_b)
+            refill_chunk(cc, cc < AP ? kt + 1 + PFA : kt + 1 + PFB, sa, sb);
+        }
       }
     }
   };
 
-  // prologue: tile 0 into LDS stage 0, then tiles 1 .. PFA (A) and 1 .. PFB (B)
-  // in flight
+  // prologue: tile 0 complete in stage 0; DMA tiles 1 .. NS-2; ring tiles
+  // 1 .. PFA / PFB in flight
   fetch_a(0, 0);
   fetch_b(0, 0);
+  dma(0, 0);
 #pragma unroll
   for (int c = 0; c < AP + BP; ++c) stash_chunk(c, 0, 0, smem);
 #pragma unroll
+  for (int t = 1; t <= NS - 2; ++t)
+    if (t < nkt) dma(t, t);
+#pragma unroll
   for (int p = 1; p <= PFA; ++p)
-    if (p < nkt) fetch_a(p, p % PFA);
+    if (AP > 0 && p < nkt) fetch_a(p, p % PFA);
 #pragma unroll
   for (int p = 1; p <= PFB; ++p)
-    if (p < nkt) fetch_b(p, p % PFB);
-  __syncthreads();
+    if (BP > 0 && p < nkt) fetch_b(p, p % PFB);
+  // loads issued after tile 0's DMA: the DMA of tiles 1 .. NS-2 and the ring
+  // fetches; count only what is certainly there (a smaller count waits longer)
+  if (nkt > NS + PFA) wait_vm_lds<(NS - 2) * D + PFA * FA + PFB * FB>();
+  else wait_vm_lds<0>();
+  lds_barrier();
 
   for (int k0 = 0; k0 < nkt; k0 += PFA) {
 #pragma unroll
@@ -285,12 +386,15 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
       if (kt < nkt) {
         // ring slots of tile kt + 1 (k0 is a multiple of PFA, hence of PFB)
         const int sa = (p + 1) % PFA, sb = (p + 1) % PFB;
-        // stage (kt + 1) & 1 was last read while computing tile kt - 1, which
-        // every wave finished before the previous barrier
-        compute(kt, kt + 1 < nkt, sa, sb);
-        if (kt + 1 + PFA < nkt) fetch_a(kt + 1 + PFA, sa);
-        if (kt + 1 + PFB < nkt) fetch_b(kt + 1 + PFB, sb);
-        __syncthreads();
+        // stage (kt + NS - 1) % NS held tile kt - 1, which every wave finished
+        // reading before the barrier that ended the previous iteration
+        compute(kt, sa, sb);
+        if (kt + 1 < nkt) {
+          // tile kt + 1 must be in LDS: its DMA and this wave's LDS stores
+          if (kt + NS + PFA + 1 < nkt) wait_vm_lds<kVmAfter>();
+          else wait_vm_lds<0>();
+        }
+        lds_barrier();
       }
     }
   }
@@ -415,11 +519,9 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
   typedef typename Elt::T T;
   constexpr int BM = kFrontBM, EP = 32 * NR;
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-  // x streams from HBM once: its ring holds PFA tiles (2 chunks per thread
-  // each). The weight rows come from L2: one tile ahead, or two when a thread's
-  // share is small enough that two sets do not spill.
-  constexpr int kBChunks = (R3 + EP) * 8 / (64 * NW);
-  typedef Tile<BM, R3, EP, 1, NW, PFA, (kBChunks > 10 || PFA % 2 != 0 ? 1 : 2)> TL;
+  // x streams from HBM once: a register ring holds PFA of its K tiles (two
+  // chunks per thread each). The weight rows come from L2 by DMA into LDS.
+  typedef Tile<BM, R3, EP, 1, NW, PFA, 1, 2, false, true> TL;
   constexpr int FM = TL::FM;   // 2: all 64 rows
   typedef RouterExtra<Elt, FM, NR, NW> RX;
   // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
@@ -608,10 +710,12 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
 }
 
 // ---- k_core: mid = (c (x) z) core_flat  (model.py:87-98) ------------------
-template <class Elt, int BM, int BN, int WM, int WN, int PFA, int PFB>
+// A (c (x) z) is formed in registers on its way to LDS (a ring of PFA tiles);
+// B (core^T) arrives by DMA.
+template <class Elt, int BM, int BN, int WM, int WN, int PFA>
 __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
   typedef typename Elt::T T;
-  typedef Tile<BM, BN, 0, WM, WN, PFA, PFB> TL;
+  typedef Tile<BM, BN, 0, WM, WN, PFA, 1, 2, false, true> TL;
   __shared__ u32x4 smem[cmax(TL::kLdsBytes, TileStage<TL, T>::kBytes) / 16];
 
   const int ntn = (int)((a.r2 + BN - 1) / BN);
@@ -642,10 +746,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
 }
 
 // ---- k_outproj: out = mid U_out + bias  (model.py:101) --------------------
-template <class Elt, int BM, int BN, int WM, int WN, int PFA, int PFB>
+// Both operands arrive by DMA through NS LDS stages.
+template <class Elt, int BM, int BN, int WM, int WN, int NS>
 __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
   typedef typename Elt::T T;
-  typedef Tile<BM, BN, 0, WM, WN, PFA, PFB> TL;
+  typedef Tile<BM, BN, 0, WM, WN, 1, 1, NS, true, true> TL;
   __shared__ u32x4 smem[cmax(TL::kLdsBytes, TileStage<TL, T>::kBytes) / 16];
 
   const int ntn = (int)((a.d_out + BN - 1) / BN);
