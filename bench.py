@@ -46,6 +46,20 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def traffic_per_launch(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary
+    (profiles/tmoe_forward_<workload>_traffic.md, line 'traffic_bytes <kernel> <bytes>'),
+    or None when it has not been measured."""
+    path = os.path.join(ROOT, "profiles", f"tmoe_forward_{workload}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.strip().strip("`").split()
+        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
+            return float(f[2])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -58,6 +72,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU work of the host baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the timed work, copy a buffer of this many MiB 3 times (a plain "
+                         "copy kernel of known size, to scale profiler byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -153,11 +170,16 @@ def main():
     log(f"[bench] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak; "
         f"layer {layer_tflops:.1f} TFLOP/s = {layer_tflops / peak:.3f} of peak")
 
-    traffic = None
-    tr_path = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
-    if os.path.exists(tr_path) and T == pkg.WORKLOADS[w.name].T:
-        with open(tr_path) as f:
-            traffic = json.load(f).get(dom)
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 3 x {args.copy_calibration_mib} MiB device copies")
+
+    traffic = traffic_per_launch(w.name, dom) if T == pkg.WORKLOADS[w.name].T else None
 
     # -- parity on a slice (GPU result of set 0 vs the fp32 reference path) --------
     from oracle import tucker_moe_np as onp
