@@ -153,13 +153,12 @@ struct KhatriRaoLoader {
 // wn*BN/WN.. of the tile as FM x FN blocks of 32 x 32. BX further B rows are
 // staged with the tile for an `extra` consumer (the router columns of k_front).
 //
-// LDS holds NS stages of [BM + BN + BX rows][8 chunks of 16 B]; chunk ch of row
-// r sits at slot ch ^ (r & 7), so the rows one fragment read touches spread over
-// all banks. Each operand reaches LDS one of two ways:
+// LDS holds NS stages of [BM + BN + BX rows][8 chunks of 16 B], XOR-swizzled
+// (lds_slot). Each operand reaches LDS one of two ways:
 //  * DMA (ADMA / BDMA): global_load_lds_dwordx4 writes LDS directly; one wave
-//    instruction fills one 1 KB block of 8 rows, lane l fetching logical chunk
-//    (l & 7) ^ (l >> 3) so the swizzle is kept. Tile kt + NS - 1 is issued
-//    while tile kt is computed.
+//    instruction fills one 1 KB block of 8 rows, each lane fetching the logical
+//    chunk its slot holds (dma_chunk). Tile kt + NS - 1 is issued while tile kt
+//    is computed.
 //  * a register ring of PFA / PFB tiles (for an operand that is transformed on
 //    the way, or streamed from HBM and wanting more tiles in flight); tile kt+1
 //    is written to LDS in between the MFMAs of tile kt.
@@ -203,11 +202,22 @@ __device__ __forceinline__ void wait_vm_lds() {
 // accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);   // no instruction is scheduled across it
   __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ int lds_slot(int row, int ch) { return row * 8 + (ch ^ (row & 7)); }
+// Chunk ch of tile row r lives at slot ch ^ ((r >> 1) & 7) of the row. A 32x32
+// fragment read touches rows r0 .. r0 + 31 at one chunk; with this swizzle any 16
+// consecutive of them fall on 16 distinct 16-byte bank groups (measured: no LDS
+// bank conflicts, against half the LDS cycles lost with a (r & 7) swizzle).
+__device__ __forceinline__ int lds_slot(int row, int ch) { return row * 8 + (ch ^ ((row >> 1) & 7)); }
+// For a DMA of 8-row block blk, lane l writes slot 64 blk + l: row 8 blk + (l >> 3),
+// physical chunk l & 7, which holds this logical chunk.
+__device__ __forceinline__ int dma_chunk(int lane, int blk) {
+  return (lane & 7) ^ ((lane >> 4) | ((blk & 1) << 2));
+}
 
 struct NoExtra {
   template <class AF>
@@ -277,18 +287,21 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
   // first, then B blocks)
   auto dma_one = [&](int j, int kt, int stage) __attribute__((always_inline)) {
     u32x4* s = smem + stage * TL::kStage;
-    const int lc = (lane & 7) ^ (lane >> 3);
     if (j < ADN) {
       if constexpr (ADMA) {
         const int blk = wave + j * W;
-        __builtin_amdgcn_global_load_lds((gbl_cvptr)aload.gaddr(blk * 8 + (lane >> 3), lc, kt),
-                                         (lds_vptr)(s + blk * 64), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            (gbl_cvptr)aload.gaddr(blk * 8 + (lane >> 3), dma_chunk(lane, blk), kt),
+            (lds_vptr)(s + blk * 64), 16, 0, 0);
       }
     } else if (j < ADN + BDN) {
       if constexpr (BDMA) {
+        // kARows is a multiple of 16, so the block parity within B equals the
+        // parity of its LDS block
         const int blk = wave + (j - ADN) * W;
-        __builtin_amdgcn_global_load_lds((gbl_cvptr)bload.gaddr(blk * 8 + (lane >> 3), lc, kt),
-                                         (lds_vptr)(s + (kARows + blk * 8) * 8), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            (gbl_cvptr)bload.gaddr(blk * 8 + (lane >> 3), dma_chunk(lane, blk), kt),
+            (lds_vptr)(s + (kARows + blk * 8) * 8), 16, 0, 0);
       }
     }
   };
@@ -398,6 +411,92 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
       }
     }
   }
+}
+
+// ---- ping-pong main loop (both operands by DMA, 8 waves) ----------------
+// Waves 0-3 (group 0) and 4-7 (group 1) sit one of each on every SIMD. Group 1
+// starts one barrier late, so the two alternate between a memory phase (read
+// all of tile kt's fragments into registers; group 0 also issues the DMA of
+// tile kt + 1) and a compute phase (the tile's MFMAs, from registers): while
+// one wave of a SIMD issues MFMAs, the other issues its memory instructions.
+// With phase p lying between barriers p - 1 and p:
+//   group 0: memory(kt) = phase 2kt, compute(kt) = phase 2kt + 1
+//   group 1: memory(kt) = phase 2kt + 1, compute(kt) = phase 2kt + 2
+// DMA(kt + 1) is issued in phase 2kt into the stage of tile kt - 1, whose last
+// reader (group 1, phase 2kt - 1) waited for its LDS reads before barrier
+// 2kt - 1; group 0 waits for the DMA at the end of phase 2kt + 1, before either
+// group reads tile kt + 1.
+template <class TL, class Elt, class ALoad, class BLoad>
+__device__ __forceinline__ void gemm_mainloop_pingpong(f32x16 (&acc)[TL::FM][TL::FN],
+                                                       const ALoad& aload, const BLoad& bload,
+                                                       int nkt, u32x4* smem) {
+  constexpr int FM = TL::FM, FN = TL::FN;
+  constexpr int kKSteps = kTileKBytes / 32;
+  constexpr int kARows = TL::BM, kBRows = TL::kBRows;
+  constexpr int kABlk = kARows / 8, kBBlk = kBRows / 8;   // 1 KB DMA blocks per tile
+  static_assert(TL::kThreads == 512 && TL::NS == 2 && TL::BX == 0, "ping-pong: 8 waves, 2 stages");
+  static_assert((kABlk + kBBlk) % 4 == 0, "DMA blocks split over group 0's four waves");
+  constexpr int kDmaPerWave = (kABlk + kBBlk) / 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = wave >> 2;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = zero16();
+
+  auto dma_block = [&](int blk, int kt, int stage) __attribute__((always_inline)) {
+    u32x4* s = smem + stage * TL::kStage;
+    const int lc = dma_chunk(lane, blk);   // kABlk is even: block parity is kept
+    if (blk < kABlk)
+      __builtin_amdgcn_global_load_lds((gbl_cvptr)aload.gaddr(blk * 8 + (lane >> 3), lc, kt),
+                                       (lds_vptr)(s + blk * 64), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds(
+          (gbl_cvptr)bload.gaddr((blk - kABlk) * 8 + (lane >> 3), lc, kt),
+          (lds_vptr)(s + (kARows + (blk - kABlk) * 8) * 8), 16, 0, 0);
+  };
+
+  // prologue: tile 0 by all eight waves
+  for (int blk = wave; blk < kABlk + kBBlk; blk += 8) dma_block(blk, 0, 0);
+  wait_vm_lds<0>();
+  lds_barrier();
+  if (grp == 1) lds_barrier();
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const u32x4* s = smem + (kt & 1) * TL::kStage;
+    // -- memory phase ---------------------------------------------------------
+    u32x4 af[kKSteps][FM], bfr[kKSteps][FN];
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) {
+      const int ch = ks * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[ks][i] = s[lds_slot(wm * TL::kWaveM + i * 32 + (lane & 31), ch)];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[ks][j] = s[lds_slot(kARows + wn * TL::kWaveN + j * 32 + (lane & 31), ch)];
+    }
+    if (grp == 0 && kt + 1 < nkt) {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) dma_block(wave + 4 * j, kt + 1, (kt + 1) & 1);
+    }
+    wait_vm_lds<63>();   // this wave's fragment reads (lgkmcnt 0); DMA stays in flight
+    lds_barrier();
+    // -- compute phase --------------------------------------------------------
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], af[ks][i], bfr[ks][j], Elt{});
+    if (grp == 0) wait_vm_lds<0>();   // DMA of tile kt + 1 has landed
+    lds_barrier();
+  }
+  if (grp == 0) lds_barrier();
 }
 
 // Work-group -> tile order for 2-D grids launched as 1-D. Consecutive
@@ -765,8 +864,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
   RowLoader bl{reinterpret_cast<const char*>(a.uoutT) + n0 * row_bytes, row_bytes,
                (int)(a.d_out - n0)};
   f32x16 acc[TL::FM][TL::FN];
-  NoExtra nx;
-  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, nx);
+  if constexpr (TL::kThreads == 512 && NS == 2) {
+    gemm_mainloop_pingpong<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem);
+  } else {
+    NoExtra nx;
+    gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, nx);
+  }
 
   char* stage = reinterpret_cast<char*>(smem);
   const int cols_valid = (int)(a.d_out - n0);
