@@ -567,8 +567,10 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 // ---- k_front: in-projection + RMSNorm, router + top-k + softmax + c --------
 // model.py:75-81 (+ the U_expert gather of :93 folded into c). One work-group:
-// 64 tokens x (R3 z columns + EP router columns), NW = R3 / 32 (at most 4) waves
-// side by side over the z columns, each owning all 64 rows.
+// BM tokens x (R3 z columns + EP router columns), NW = R3 / 32 (at most 4) waves
+// side by side over the z columns, each owning all BM rows. BM = 32 keeps the
+// LDS under 80 KB, so two work-groups share a CU and one's epilogue overlaps
+// the other's main loop.
 //  z part: epilogue z = (z / rms) * g with rms = sqrt(mean(z^2) + eps)
 //  (model.py:25-27), the division taken as a multiply by 1 / rms.
 //  router part (NR = EP/32 column blocks): with NR < NW every wave computes all
@@ -613,15 +615,15 @@ struct RouterExtra {
   }
 };
 
-template <class Elt, int R3, int NR, int PFA = kFrontPFA>
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM>
 __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
   typedef typename Elt::T T;
-  constexpr int BM = kFrontBM, EP = 32 * NR;
+  constexpr int EP = 32 * NR;
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
   // x streams from HBM once: a register ring holds PFA of its K tiles (two
   // chunks per thread each). The weight rows come from L2 by DMA into LDS.
   typedef Tile<BM, R3, EP, 1, NW, PFA, 1, 2, false, true> TL;
-  constexpr int FM = TL::FM;   // 2: all 64 rows
+  constexpr int FM = TL::FM;   // every wave covers all BM rows
   typedef RouterExtra<Elt, FM, NR, NW> RX;
   // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
   constexpr int LD = EP + 1;
