@@ -93,18 +93,31 @@ def main():
     w = pkg.WORKLOADS[args.workload]
     if args.tokens:
         w = w.with_T(args.tokens)
-    if w.fp8:
-        raise SystemExit(f"workload {w.name} (fp8) is not implemented yet")
     T = w.T
     dev = torch.device("cuda:0")
     dt_name = "bf16" if w.dtype == torch.bfloat16 else "f32"
     es = 2 if w.dtype == torch.bfloat16 else 4
 
     # -- model and rotated buffer sets -----------------------------------------
-    params = pkg.synth.make_params(w)
+    from oracle import e4m3
+    if w.fp8:
+        # e4m3 U_in / core / U_out + per-output-channel scales; the reference layer
+        # is run on the dequantised weights (the oracle's e4m3 decoding)
+        params, codes, _ = pkg.synth.make_fp8_params(w)
+        ref_params = {k: v.float() for k, v in params.items()}
+        for k in ("U_in", "core", "U_out"):
+            ref_params[k] = torch.from_numpy(e4m3.dequantize(
+                codes[f"{k}_q"].view(torch.uint8).numpy(), codes[f"{k}_scale"].double().numpy(),
+                k)).float()
+    else:
+        params = pkg.synth.make_params(w)
+        codes, ref_params = None, params
     x0 = pkg.synth.make_x(w)
     m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
     m.load_state_dict({k: v.to(dev) for k, v in params.items()})
+    if codes is not None:
+        m.load_fp8(*[codes[k].to(dev) for k in ("U_in_q", "U_in_scale", "core_q", "core_scale",
+                                                  "U_out_q", "U_out_scale")])
     plan = m.plan()
     packed0 = m.packed()
     ws_bytes = plan.workspace_bytes(T)
@@ -191,13 +204,14 @@ def main():
                                   s0["out"].data_ptr(), idx.data_ptr(), None, None,
                                   s0["ws"].data_ptr(), ws_bytes, sptr))
     torch.cuda.synchronize()
-    ref = ot.forward(x0[:n_par], params, w.k, compute_dtype=torch.float32, intermediates=True)
+    ref = ot.forward(x0[:n_par], ref_params, w.k, compute_dtype=torch.float32, intermediates=True)
     parity = {
         "tokens": n_par,
         "rel_l2_out": onp.rel_l2(s0["out"][:n_par].float().cpu().numpy(), ref["out"].double().numpy()),
         "topk_idx_equal": bool(torch.equal(idx[:n_par].long().cpu(), ref["idx"])),
         "min_topk_gap": float(onp.topk_gap(ref["logits"].double().numpy(), w.k).min()),
-        "reference": "oracle/tucker_moe_torch fp32 on the bf16-valued inputs",
+        "reference": "oracle/tucker_moe_torch fp32 on the bf16-valued inputs"
+                     + (" and the dequantised e4m3 weights" if w.fp8 else ""),
     }
     log(f"[bench] parity on {n_par} tokens: {parity}")
 
@@ -208,6 +222,8 @@ def main():
         chunk = 512
         xs = x0[:chunk]
         t_a = time.perf_counter()
+        # fp8: the reference runs on the dequantised weights, held in bf16 as the
+        # module's parameters hold them
         ot.forward(xs, params, w.k, chunk=chunk)            # warm-up, also sizes the sample
         rate = chunk / (time.perf_counter() - t_a)
         n_cpu = int(min(T, max(chunk, args.cpu_seconds * rate)) // chunk * chunk)
@@ -238,7 +254,9 @@ def main():
         "data": "synthetic (seeded N(0,1) tokens, N(0,1/fan_in) weights; no checkpoint)",
         "config": {"workload": f"{w.name}: Tucker-MoE layer forward, one GPU", "T": T,
                    "d_in": w.d_in, "d_out": w.d_out, "E": w.E, "top_k": w.k,
-                   "r1": w.r1, "r3": w.r3, "r2": w.r2, "rotated_sets": n_sets},
+                   "r1": w.r1, "r3": w.r3, "r2": w.r2, "rotated_sets": n_sets,
+                   "weights": ("U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales, "
+                               "unpacked exactly to bf16; bf16 MFMA" if w.fp8 else dt_name)},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,
                      "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
                      "avg_us": stage_avg_us[dom], "flops_per_launch": fl[dom]},

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 1
+#define TMOE_ABI_VERSION 2
 
 /* error codes */
 #define TMOE_OK            0
@@ -44,6 +44,11 @@ extern "C" {
 /* element types */
 #define TMOE_F32  0
 #define TMOE_BF16 1
+/* bf16 activations, output, router_w, inner_w, U_expert and bias; U_in, core and
+ * U_out as OCP fp8 e4m3 with one fp32 scale per output channel (packed by
+ * tmoe_pack_weights_fp8). The kernels convert e4m3 to bf16 exactly and compute as
+ * for TMOE_BF16, applying the scales in fp32. */
+#define TMOE_BF16_FP8W 2
 
 /* Layer hyper-parameters.
  * Replaces TuckerMoE.__init__(d_in, d_out, cfg) (model.py:54-66):
@@ -54,7 +59,8 @@ typedef struct tmoe_shape {
   int64_t d_in, d_out;
   int64_t E, k;
   int64_t r1, r2, r3;
-  int32_t dtype;   /* TMOE_BF16 or TMOE_F32: activations, weights and output */
+  int32_t dtype;   /* TMOE_BF16 or TMOE_F32: activations, weights and output;
+                      TMOE_BF16_FP8W: bf16 activations, e4m3 projection weights */
   float   eps;
 } tmoe_shape;
 
@@ -92,6 +98,24 @@ int tmoe_pack_weights(const tmoe_plan* plan,
                       const void* router_w, const void* U_in, const void* inner_w,
                       const void* U_expert, const void* core, const void* U_out,
                       const void* bias, void* packed, void* stream);
+
+/* tmoe_pack_weights for a TMOE_BF16_FP8W plan (TMOE_EINVAL for any other plan,
+ * and tmoe_pack_weights gives TMOE_EINVAL for this one). The reference has no
+ * fp8 parameters: the layer it computes is TuckerMoE (model.py:60-66) with the
+ * dequantised weights
+ *   U_in[i, j]     = e4m3(U_in_q[i, j])     * U_in_scale[j]          (d_in, r3), scales (r3)
+ *   core[r, s, q]  = e4m3(core_q[r, s, q])  * core_scale[r * r2 + q] (r1, r3, r2), scales (r1, r2)
+ *   U_out[i, n]    = e4m3(U_out_q[i, n])    * U_out_scale[n]         (r2, d_out), scales (d_out)
+ * i.e. one scale per output channel of each projection (for core, per column of
+ * its (r3, r1*r2) matrix view). e4m3 is OCP FP8 E4M3 (bias 7, no infinities,
+ * 0x7f / 0xff are NaN). router_w, inner_w, U_expert and bias are bf16. Scales
+ * must be finite; a zero scale zeroes its channel. */
+int tmoe_pack_weights_fp8(const tmoe_plan* plan, const void* router_w,
+                          const uint8_t* U_in_q, const float* U_in_scale,
+                          const void* inner_w, const void* U_expert,
+                          const uint8_t* core_q, const float* core_scale,
+                          const uint8_t* U_out_q, const float* U_out_scale,
+                          const void* bias, void* packed, void* stream);
 
 /* The layer forward for T tokens: out = TuckerMoE.forward(x) (model.py:68-102).
  *   x        (T, d_in)   plan dtype

@@ -7,11 +7,12 @@ Public surface:
   WORKLOADS                    the named seeded workloads C1..C5 (config.py)
   load_tucker                  checkpoint-key loader that refreshes packed weights
   synth                        seeded synthetic parameters and tokens
+  fp8                          e4m3 weights with per-output-channel scales
   _lib                         ctypes binding of the C ABI (include/tmoe.h)
 """
-from . import _lib, config, synth
+from . import _lib, config, fp8, synth
 from .config import WORKLOADS, TuckerMoEConfig, Workload
 from .module import RMSNorm, TuckerMoE, load_tucker
 
 __all__ = ["TuckerMoE", "RMSNorm", "TuckerMoEConfig", "Workload", "WORKLOADS", "load_tucker",
-           "synth", "config", "_lib"]
+           "synth", "config", "fp8", "_lib"]

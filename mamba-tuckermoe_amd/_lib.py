@@ -19,16 +19,17 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
-TMOE_F32, TMOE_BF16 = 0, 1
+TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
 
 # Every function include/tmoe.h declares.
 EXPORTED = (
     "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
-    "tmoe_packed_bytes", "tmoe_workspace_bytes", "tmoe_pack_weights", "tmoe_forward",
+    "tmoe_packed_bytes", "tmoe_workspace_bytes", "tmoe_pack_weights", "tmoe_pack_weights_fp8",
+    "tmoe_forward",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
 
@@ -84,6 +85,8 @@ def lib() -> ctypes.CDLL:
         L.tmoe_workspace_bytes.argtypes = [vp, i64]
         L.tmoe_pack_weights.restype = ctypes.c_int
         L.tmoe_pack_weights.argtypes = [vp] * 10
+        L.tmoe_pack_weights_fp8.restype = ctypes.c_int
+        L.tmoe_pack_weights_fp8.argtypes = [vp] * 13
         L.tmoe_forward.restype = ctypes.c_int
         L.tmoe_forward.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]
         L.tmoe_prof_enable.restype = ctypes.c_int
@@ -108,8 +111,14 @@ def check(rc: int) -> int:
 class Plan:
     """Owns a tmoe_plan*. Immutable; safe to share across streams."""
 
-    def __init__(self, d_in, d_out, E, k, r1, r2, r3, dtype: torch.dtype, eps: float):
-        if dtype == torch.bfloat16:
+    def __init__(self, d_in, d_out, E, k, r1, r2, r3, dtype: torch.dtype, eps: float,
+                 fp8_weights: bool = False):
+        if fp8_weights:
+            if dtype != torch.bfloat16:
+                raise TmoeError(TMOE_EUNSUPPORTED,
+                                f"fp8 weights need bfloat16 activations, not {dtype}")
+            code = TMOE_BF16_FP8W
+        elif dtype == torch.bfloat16:
             code = TMOE_BF16
         elif dtype == torch.float32:
             code = TMOE_F32
@@ -118,6 +127,7 @@ class Plan:
                             f"parameter dtype {dtype}: supported are bfloat16 and float32")
         self.shape = TmoeShape(d_in, d_out, E, k, r1, r2, r3, code, eps)
         self.dtype = dtype
+        self.fp8_weights = fp8_weights
         self._ptr = ctypes.c_void_p()
         L = lib()
         check(L.tmoe_plan_create(ctypes.byref(self.shape), ctypes.byref(self._ptr)))

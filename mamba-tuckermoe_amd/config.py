@@ -63,12 +63,17 @@ class Workload:
         return st
 
     def hbm_bytes(self, T: Optional[int] = None) -> int:
-        """Compulsory HBM bytes per forward: x in, out, every weight once."""
+        """Compulsory HBM bytes per forward: x in, out, every weight once (fp8
+        workloads: the three projections at one byte plus their fp32 scales)."""
         T = self.T if T is None else T
         es = 4 if self.dtype == torch.float32 else 2
-        w = (self.E * self.d_in + self.d_in * self.r3 + self.r3 + self.E * self.r1
-             + self.r1 * self.r3 * self.r2 + self.r2 * self.d_out + self.d_out)
-        return T * self.d_in * es + T * self.d_out * es + w * es
+        small = self.E * self.d_in + self.r3 + self.E * self.r1 + self.d_out
+        proj = self.d_in * self.r3 + self.r1 * self.r3 * self.r2 + self.r2 * self.d_out
+        if self.fp8:
+            wbytes = small * es + proj + 4 * (self.r3 + self.r1 * self.r2 + self.d_out)
+        else:
+            wbytes = (small + proj) * es
+        return T * self.d_in * es + T * self.d_out * es + wbytes
 
 
 WORKLOADS = {

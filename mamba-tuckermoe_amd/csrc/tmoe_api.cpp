@@ -19,10 +19,14 @@
 struct tmoe_plan {
   tmoe_shape s;
   int64_t E_pad;
-  size_t es;   // element size of the plan dtype
+  size_t es;     // element size of the activations (and of the packed weights)
+  bool fp8w;     // TMOE_BF16_FP8W: weights arrive as e4m3 + scales, kernels run bf16
+  int kdtype;    // dtype the kernels compute in (TMOE_BF16 / TMOE_F32)
   // packed-weight layout (byte offsets); the front operand is U_in^T (r3 rows)
-  // immediately followed by the router rows (E_pad rows, zero past E)
-  size_t off_front, off_router, off_gain, off_uexp, off_core, off_uout, off_bias, packed_bytes;
+  // immediately followed by the router rows (E_pad rows, zero past E). fp8 plans
+  // add the U_in column scales, the core scale table and the U_out column scales.
+  size_t off_front, off_router, off_gain, off_uexp, off_core, off_uout, off_bias;
+  size_t off_sin, off_cscale, off_sout, packed_bytes;
 };
 
 namespace {
@@ -96,8 +100,8 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   if (!shape || !plan_out) return fail(TMOE_EINVAL, "tmoe_plan_create: null argument");
   *plan_out = nullptr;
   const tmoe_shape& s = *shape;
-  if (s.dtype != TMOE_BF16 && s.dtype != TMOE_F32)
-    return fail(TMOE_EINVAL, "dtype %d is neither TMOE_BF16 nor TMOE_F32", s.dtype);
+  if (s.dtype != TMOE_BF16 && s.dtype != TMOE_F32 && s.dtype != TMOE_BF16_FP8W)
+    return fail(TMOE_EINVAL, "dtype %d is not TMOE_BF16, TMOE_F32 or TMOE_BF16_FP8W", s.dtype);
   if (s.d_in <= 0 || s.d_out <= 0 || s.E <= 0 || s.k <= 0 || s.r1 <= 0 || s.r2 <= 0 || s.r3 <= 0)
     return fail(TMOE_EINVAL,
                 "dimensions must be positive (d_in=%lld d_out=%lld E=%lld k=%lld r=(%lld,%lld,%lld))",
@@ -127,7 +131,9 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   tmoe_plan* p = new (std::nothrow) tmoe_plan();
   if (!p) return fail(TMOE_EINVAL, "out of host memory");
   p->s = s;
-  p->es = s.dtype == TMOE_BF16 ? 2 : 4;
+  p->fp8w = s.dtype == TMOE_BF16_FP8W;
+  p->kdtype = s.dtype == TMOE_F32 ? TMOE_F32 : TMOE_BF16;
+  p->es = p->kdtype == TMOE_BF16 ? 2 : 4;
   int64_t ep = 32;
   while (ep < s.E) ep *= 2;   // router column blocks of 32: widths 32, 64, 128, 256
   p->E_pad = ep;
@@ -140,6 +146,12 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   p->off_core = o; o = align256(o + (size_t)s.r2 * s.r1 * s.r3 * p->es);
   p->off_uout = o; o = align256(o + (size_t)s.d_out * s.r2 * p->es);
   p->off_bias = o; o = align256(o + (size_t)s.d_out * sizeof(float));
+  p->off_sin = p->off_cscale = p->off_sout = 0;
+  if (p->fp8w) {
+    p->off_sin = o;    o = align256(o + (size_t)s.r3 * sizeof(float));
+    p->off_cscale = o; o = align256(o + (size_t)s.r1 * s.r2 * sizeof(float));
+    p->off_sout = o;   o = align256(o + (size_t)s.d_out * sizeof(float));
+  }
   p->packed_bytes = o;
   *plan_out = p;
   return TMOE_OK;
@@ -159,6 +171,9 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
                       const void* U_out, const void* bias, void* packed, void* stream) {
   g_err[0] = 0;
   if (!p) return fail(TMOE_EINVAL, "tmoe_pack_weights: null plan");
+  if (p->fp8w)
+    return fail(TMOE_EINVAL, "tmoe_pack_weights: a TMOE_BF16_FP8W plan is packed by "
+                             "tmoe_pack_weights_fp8");
   const void* ptrs[] = {router_w, U_in, inner_w, U_expert, core, U_out, bias, packed};
   const char* names[] = {"router_w", "U_in", "inner_w", "U_expert", "core", "U_out", "bias",
                          "packed"};
@@ -195,6 +210,61 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
   return TMOE_OK;
 }
 
+int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_t* U_in_q,
+                          const float* U_in_scale, const void* inner_w, const void* U_expert,
+                          const uint8_t* core_q, const float* core_scale,
+                          const uint8_t* U_out_q, const float* U_out_scale, const void* bias,
+                          void* packed, void* stream) {
+  g_err[0] = 0;
+  if (!p) return fail(TMOE_EINVAL, "tmoe_pack_weights_fp8: null plan");
+  if (!p->fp8w)
+    return fail(TMOE_EINVAL, "tmoe_pack_weights_fp8: the plan's dtype is not TMOE_BF16_FP8W");
+  const void* ptrs[] = {router_w, U_in_q, U_in_scale, inner_w, U_expert, core_q,
+                        core_scale, U_out_q, U_out_scale, bias, packed};
+  const char* names[] = {"router_w", "U_in_q", "U_in_scale", "inner_w", "U_expert", "core_q",
+                         "core_scale", "U_out_q", "U_out_scale", "bias", "packed"};
+  for (int i = 0; i < 11; ++i)
+    if (!ptrs[i]) return fail(TMOE_EINVAL, "tmoe_pack_weights_fp8: %s is null", names[i]);
+  if (!aligned16(packed))
+    return fail(TMOE_EINVAL, "tmoe_pack_weights_fp8: packed is not 16-byte aligned");
+  const tmoe_shape& s = p->s;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(packed);
+  auto f32at = [&](size_t off) { return reinterpret_cast<float*>(base + off); };
+  auto bf16at = [&](size_t off) { return reinterpret_cast<uint16_t*>(base + off); };
+  hipError_t e;
+  if ((e = tmoe::launch_transpose_e4m3(U_in_q, bf16at(p->off_front), s.d_in, s.r3, nullptr, 1,
+                                       st)) != hipSuccess)
+    return hip_fail(e, "pack U_in");
+  if ((e = tmoe::launch_copy_pad(router_w, base + p->off_router, s.E * s.d_in,
+                                 p->E_pad * s.d_in, 2, st)) != hipSuccess)
+    return hip_fail(e, "pack router");
+  if ((e = tmoe::launch_to_f32(inner_w, f32at(p->off_gain), s.r3, TMOE_BF16, st)) != hipSuccess)
+    return hip_fail(e, "pack inner_norm.weight");
+  if ((e = tmoe::launch_to_f32(U_expert, f32at(p->off_uexp), s.E * s.r1, TMOE_BF16, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack U_expert");
+  // core (r1, r3, r2) -> (r2, r1*r3); channel (r, q) of row r*r3 + s, column q
+  if ((e = tmoe::launch_transpose_e4m3(core_q, bf16at(p->off_core), s.r1 * s.r3, s.r2,
+                                       core_scale, s.r3, st)) != hipSuccess)
+    return hip_fail(e, "pack core");
+  if ((e = tmoe::launch_core_scales(core_scale, f32at(p->off_cscale), s.r1, s.r2, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack core scales");
+  if ((e = tmoe::launch_transpose_e4m3(U_out_q, bf16at(p->off_uout), s.r2, s.d_out, nullptr, 1,
+                                       st)) != hipSuccess)
+    return hip_fail(e, "pack U_out");
+  if ((e = tmoe::launch_to_f32(bias, f32at(p->off_bias), s.d_out, TMOE_BF16, st)) != hipSuccess)
+    return hip_fail(e, "pack bias");
+  if ((e = tmoe::launch_to_f32(U_in_scale, f32at(p->off_sin), s.r3, TMOE_F32, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack U_in scales");
+  if ((e = tmoe::launch_to_f32(U_out_scale, f32at(p->off_sout), s.d_out, TMOE_F32, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack U_out scales");
+  return TMOE_OK;
+}
+
 int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
                  int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
                  size_t workspace_bytes, void* stream) {
@@ -217,7 +287,7 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   char* ws = static_cast<char*>(workspace);
 
   tmoe::FwdArgs a{};
-  a.dtype = s.dtype;
+  a.dtype = p->kdtype;
   a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
   a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
   a.x = x;
@@ -227,6 +297,11 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.coreT = pk + p->off_core;
   a.uoutT = pk + p->off_uout;
   a.bias = reinterpret_cast<const float*>(pk + p->off_bias);
+  if (p->fp8w) {
+    a.zscale = reinterpret_cast<const float*>(pk + p->off_sin);
+    a.core_scale = reinterpret_cast<const float*>(pk + p->off_cscale);
+    a.out_scale = reinterpret_cast<const float*>(pk + p->off_sout);
+  }
   a.out = out;
   a.idx = topk_idx ? topk_idx : reinterpret_cast<int32_t*>(ws + L.idx);
   a.w = topk_w ? topk_w : reinterpret_cast<float*>(ws + L.w);

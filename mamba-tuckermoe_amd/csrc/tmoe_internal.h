@@ -30,6 +30,10 @@ struct FwdArgs {
   const void* coreT;            // (r2, r1*r3)          core as (r1*r3, r2), transposed
   const void* uoutT;            // (d_out, r2)          U_out transposed
   const float* bias;            // (d_out)
+  // fp8-weight plans only (null otherwise): per-output-channel scales
+  const float* zscale;          // (r3)                 U_in column scales
+  const float* core_scale;      // (r1, r2)             rank-change ratios, last rank's scales
+  const float* out_scale;       // (d_out)              U_out column scales
   // outputs / workspace
   void* out;
   int32_t* idx;                 // (T, k)
@@ -46,6 +50,13 @@ hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
 
 // Weight packing helpers (stream-ordered).
+// dst(cols, rows) bf16 = e4m3 src(rows, cols)^T; with colscale, entries whose
+// scale colscale[(row / group) * cols + col] is zero are stored as zero.
+hipError_t launch_transpose_e4m3(const uint8_t* src, uint16_t* dst, int64_t rows, int64_t cols,
+                                 const float* colscale, int64_t group, hipStream_t stream);
+// core scale table (r1, r2) from the per-channel scales sc (r1, r2)
+hipError_t launch_core_scales(const float* sc, float* cs, int64_t r1, int64_t r2,
+                              hipStream_t stream);
 // dst(cols, rows) = src(rows, cols)^T, element size es (2 or 4 bytes).
 hipError_t launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int es,
                             hipStream_t stream);

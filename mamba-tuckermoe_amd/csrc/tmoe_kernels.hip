@@ -87,6 +87,23 @@ hipError_t launch_transpose(const void* src, void* dst, int64_t rows, int64_t co
   return hipGetLastError();
 }
 
+hipError_t launch_transpose_e4m3(const uint8_t* src, uint16_t* dst, int64_t rows, int64_t cols,
+                                 const float* colscale, int64_t group, hipStream_t st) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const dim3 grid(cdiv(cols, 32), cdiv(rows, 32)), block(256);
+  hipLaunchKernelGGL(dev::k_transpose_e4m3, grid, block, 0, st, src, dst, rows, cols, colscale,
+                     group);
+  return hipGetLastError();
+}
+
+hipError_t launch_core_scales(const float* sc, float* cs, int64_t r1, int64_t r2,
+                              hipStream_t st) {
+  if (r1 == 0 || r2 == 0) return hipSuccess;
+  const dim3 grid(cdiv(r2, 256) < 1024 ? cdiv(r2, 256) : 1024), block(256);
+  hipLaunchKernelGGL(dev::k_core_scales, grid, block, 0, st, sc, cs, r1, r2);
+  return hipGetLastError();
+}
+
 hipError_t launch_copy_pad(const void* src, void* dst, int64_t n, int64_t n_pad, int es,
                            hipStream_t st) {
   if (n_pad == 0) return hipSuccess;

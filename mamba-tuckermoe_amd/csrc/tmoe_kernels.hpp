@@ -219,9 +219,13 @@ __device__ __forceinline__ int dma_chunk(int lane, int blk) {
   return (lane & 7) ^ ((lane >> 4) | ((blk & 1) << 2));
 }
 
+// A main-loop consumer: operator() runs after every K step's MFMAs with that
+// step's A fragments; tile_begin(kt, acc) runs before the MFMAs of K tile kt.
 struct NoExtra {
   template <class AF>
   __device__ __forceinline__ void operator()(const u32x4*, int, int, const AF&) const {}
+  template <class ACC>
+  __device__ __forceinline__ void tile_begin(int, ACC&) const {}
 };
 
 template <class TL, class Elt, class ALoad, class BLoad, class Extra>
@@ -401,6 +405,7 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
         const int sa = (p + 1) % PFA, sb = (p + 1) % PFB;
         // stage (kt + NS - 1) % NS held tile kt - 1, which every wave finished
         // reading before the barrier that ended the previous iteration
+        extra.tile_begin(kt, acc);
         compute(kt, sa, sb);
         if (kt + 1 < nkt) {
           // tile kt + 1 must be in LDS: its DMA and this wave's LDS stores
@@ -522,11 +527,13 @@ struct TileStage {
   static constexpr int kBytes = TL::BM * kRowBytes;
 };
 
-// Stores acc + colv[j] (colv: a per-column addend this lane holds for each of its
-// FN column blocks, loaded once before the loop) as T.
+// Stores acc * colm[j] + colv[j] as T (colm, colv: a per-column multiplier and
+// addend this lane holds for each of its FN column blocks, loaded once before the
+// loop). A multiplier of 1 leaves acc + colv exactly.
 template <class TL, class T>
 __device__ __forceinline__ void stage_tile(const f32x16 (&acc)[TL::FM][TL::FN], char* stage,
-                                           const float (&colv)[TL::FN]) {
+                                           const float (&colv)[TL::FN],
+                                           const float (&colm)[TL::FN]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
   constexpr int RB = TileStage<TL, T>::kRowBytes;
@@ -538,8 +545,8 @@ __device__ __forceinline__ void stage_tile(const f32x16 (&acc)[TL::FM][TL::FN], 
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = wm * TL::kWaveM + i * 32 + acc_row(lane, e);
-        store_from_f32(reinterpret_cast<T*>(stage + row * RB + col * (int)sizeof(T)),
-                       acc[i][j][e] + colv[j]);
+        const float v = acc[i][j][e] * colm[j] + colv[j];
+        store_from_f32(reinterpret_cast<T*>(stage + row * RB + col * (int)sizeof(T)), v);
       }
   }
 }
@@ -613,16 +620,18 @@ struct RouterExtra {
       for (int i = 0; i < FM; ++i) mma(racc[i][j], af[i], b, Elt{});
     }
   }
+  template <class ACC>
+  __device__ __forceinline__ void tile_begin(int, ACC&) const {}
 };
 
-template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM>
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2>
 __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
   typedef typename Elt::T T;
   constexpr int EP = 32 * NR;
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
   // x streams from HBM once: a register ring holds PFA of its K tiles (two
   // chunks per thread each). The weight rows come from L2 by DMA into LDS.
-  typedef Tile<BM, R3, EP, 1, NW, PFA, 1, 2, false, true> TL;
+  typedef Tile<BM, R3, EP, 1, NW, PFA, 1, NS, false, true> TL;
   constexpr int FM = TL::FM;   // every wave covers all BM rows
   typedef RouterExtra<Elt, FM, NR, NW> RX;
   // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
@@ -661,6 +670,18 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
         else
           lg[row * LD + (wave * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
       }
+
+  // -- fp8 weights: z column j = (x . q_in[:, j]) * s_in[j] ----------------
+  if (a.zscale) {
+#pragma unroll
+    for (int j = 0; j < TL::FN; ++j) {
+      const float sc = a.zscale[wave * TL::kWaveN + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] *= sc;
+    }
+  }
 
   // -- RMSNorm row sums of squares ------------------------------------------
   // lanes l and l ^ m (m < 32) hold the same rows
@@ -813,6 +834,51 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
 // ---- k_core: mid = (c (x) z) core_flat  (model.py:87-98) ------------------
 // A (c (x) z) is formed in registers on its way to LDS (a ring of PFA tiles);
 // B (core^T) arrives by DMA.
+// fp8 core weights G[r, s, q] = g[r, s, q] * sc[r, q] (per output channel (r, q)).
+// The K tiles of rank r (tiles_per_r consecutive ones) accumulate
+// sum_s A[t, (r, s)] g[r, s, q] unscaled; entering rank r + 1 the accumulator is
+// multiplied by cs[r, q] = sc[r, q] / sc[r + 1, q], and the epilogue multiplies by
+// cs[r1 - 1, q] = sc[r1 - 1, q], which leaves sum_r sc[r, q] * (rank r's sum).
+// The ratios of the next rank change are loaded one change ahead; columns at or
+// past r2 (a partial last tile) read nothing and keep factor 1.
+template <int FM, int FN>
+struct CoreRescale {
+  const float* cs;   // (r1, r2) as above
+  int tiles_per_r, r1, r2;
+  int colbase;       // this lane's column of block j is colbase + 32 j
+  float nxt[FN];
+  __device__ __forceinline__ void init(const float* cs_, int tpr, int r1_, int r2_, int col0) {
+    cs = cs_;
+    tiles_per_r = tpr;
+    r1 = r1_;
+    r2 = r2_;
+    colbase = col0;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      nxt[j] = (cs && r1 > 1 && colbase + 32 * j < r2) ? cs[colbase + 32 * j] : 1.f;
+  }
+  template <class AF>
+  __device__ __forceinline__ void operator()(const u32x4*, int, int, const AF&) const {}
+  template <class ACC>
+  __device__ __forceinline__ void tile_begin(int kt, ACC& acc) {
+    if (!cs || kt == 0 || kt % tiles_per_r != 0) return;
+    const int r = kt / tiles_per_r;   // entering rank r >= 1: multiply by cs[r - 1, :]
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const float f = nxt[j];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] *= f;
+    }
+    if (r + 1 < r1) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if (colbase + 32 * j < r2) nxt[j] = cs[(int64_t)r * r2 + colbase + 32 * j];
+    }
+  }
+};
+
 template <class Elt, int BM, int BN, int WM, int WN, int PFA>
 __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
   typedef typename Elt::T T;
@@ -833,14 +899,23 @@ __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
   RowLoader bl{reinterpret_cast<const char*>(a.coreT) + n0 * b_row_bytes, b_row_bytes,
                (int)(a.r2 - n0)};
   f32x16 acc[TL::FM][TL::FN];
-  NoExtra nx;
-  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(b_row_bytes / kTileKBytes), smem, nx);
+  const int wn = (threadIdx.x >> 6) % WN, lane = threadIdx.x & 63;
+  const int col0 = wn * TL::kWaveN + (lane & 31);   // column of block j: col0 + 32 j
+  CoreRescale<TL::FM, TL::FN> rs;
+  rs.init(a.core_scale, (int)(a.r3 * (int64_t)sizeof(T) / kTileKBytes), (int)a.r1, (int)a.r2,
+          (int)n0 + col0);
+  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(b_row_bytes / kTileKBytes), smem, rs);
 
   char* stage = reinterpret_cast<char*>(smem);
-  float zero[TL::FN];
+  float zero[TL::FN], last[TL::FN];
 #pragma unroll
-  for (int j = 0; j < TL::FN; ++j) zero[j] = 0.f;
-  stage_tile<TL, T>(acc, stage, zero);
+  for (int j = 0; j < TL::FN; ++j) {
+    zero[j] = 0.f;
+    const int col = col0 + 32 * j;
+    last[j] = a.core_scale && col < a.r2 - n0
+                  ? a.core_scale[(a.r1 - 1) * a.r2 + n0 + col] : 1.f;
+  }
+  stage_tile<TL, T>(acc, stage, zero, last);
   __syncthreads();
   flush_tile<TL, T>(stage, reinterpret_cast<T*>(a.mid) + m0 * a.r2 + n0, a.r2, rows_valid,
                     (int)(a.r2 - n0));
@@ -875,16 +950,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
 
   char* stage = reinterpret_cast<char*>(smem);
   const int cols_valid = (int)(a.d_out - n0);
-  float bcol[TL::FN];
+  float bcol[TL::FN], scol[TL::FN];
   {
     const int wn = (threadIdx.x >> 6) % WN, lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < TL::FN; ++j) {
       const int col = wn * TL::kWaveN + j * 32 + (lane & 31);
       bcol[j] = col < cols_valid ? a.bias[n0 + col] : 0.f;
+      scol[j] = a.out_scale && col < cols_valid ? a.out_scale[n0 + col] : 1.f;
     }
   }
-  stage_tile<TL, T>(acc, stage, bcol);
+  stage_tile<TL, T>(acc, stage, bcol, scol);
   __syncthreads();
   flush_tile<TL, T>(stage, reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0, a.d_out, rows_valid,
                     cols_valid);
@@ -905,6 +981,62 @@ __global__ void k_transpose(const T* __restrict__ src, T* __restrict__ dst, int6
   for (int y = ty; y < 32; y += 8) {
     const int64_t c = c0 + y, r = r0 + tx;   // dst row c, column r
     if (r < rows && c < cols) dst[c * rows + r] = tile[tx][y];
+  }
+}
+
+// OCP e4m3 (1-4-3, bias 7, no infinities, S.1111.111 = NaN) to bf16 bits. Every
+// e4m3 value is exactly representable in bf16.
+__device__ __forceinline__ uint16_t e4m3_to_bf16_bits(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 8;
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  if (e == 15u && m == 7u) return (uint16_t)(sign | 0x7fc0u);
+  // normal: (8 + m) 2^(e - 10); subnormal (e = 0): m 2^-9
+  const float v = e ? ldexpf((float)(8u + m), (int)e - 10) : ldexpf((float)m, -9);
+  return (uint16_t)(sign | (__float_as_uint(v) >> 16));
+}
+
+// dst (cols, rows) bf16 = e4m3 src (rows, cols) transposed. With colscale
+// (scale of (row / group, col) at colscale[(row / group) * cols + col]) an entry
+// whose scale is zero is stored as zero.
+__global__ void k_transpose_e4m3(const uint8_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                 int64_t rows, int64_t cols, const float* __restrict__ colscale,
+                                 int64_t group) {
+  __shared__ uint16_t t[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  for (int i = threadIdx.x; i < 32 * 32; i += blockDim.x) {
+    const int rr = i / 32, cc = i % 32;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    uint16_t v = 0;
+    if (r < rows && c < cols) {
+      v = e4m3_to_bf16_bits(src[r * cols + c]);
+      if (colscale && colscale[(r / group) * cols + c] == 0.f) v = 0;
+    }
+    t[rr][cc] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 32 * 32; i += blockDim.x) {
+    const int cc = i / 32, rr = i % 32;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    if (r < rows && c < cols) dst[c * rows + r] = t[rr][cc];
+  }
+}
+
+// Core scale table of CoreRescale from sc (r1, r2): cs[r, q] = sc'[r, q] /
+// sc'[r + 1, q] for r < r1 - 1 and cs[r1 - 1, q] = sc'[r1 - 1, q], where sc' is sc
+// with zeros replaced by 1 (those channels' weights are packed as zero).
+__global__ void k_core_scales(const float* __restrict__ sc, float* __restrict__ cs, int64_t r1,
+                              int64_t r2) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < r2;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    for (int64_t r = 0; r < r1; ++r) {
+      const float a = sc[r * r2 + q] == 0.f ? 1.f : sc[r * r2 + q];
+      if (r + 1 < r1) {
+        const float b = sc[(r + 1) * r2 + q] == 0.f ? 1.f : sc[(r + 1) * r2 + q];
+        cs[r * r2 + q] = a / b;
+      } else {
+        cs[r * r2 + q] = a;
+      }
+    }
   }
 }
 

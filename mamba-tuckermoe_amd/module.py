@@ -17,6 +17,14 @@ The kernels read a packed copy of the parameters. It is rebuilt when a
 parameter's storage, version counter, dtype or device changes. Writes through
 `param.data` (which the reference loader uses) do not move the version counter,
 so call refresh_packed() after such a write, or load with load_tucker() below.
+
+fp8 weights (no counterpart in the reference): load_fp8() or quantize_fp8_()
+switch a bf16 module to U_in, core and U_out held as e4m3 codes with
+per-output-channel fp32 scales (see fp8.py); the layer computed is the
+reference layer with the dequantised weights, which those calls also write
+into the parameters (rounded to bf16) so that state_dict() describes it. While
+fp8 weights are loaded they, not U_in / core / U_out, feed the kernels;
+clear_fp8() returns to the parameters.
 """
 from __future__ import annotations
 
@@ -27,6 +35,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
+from . import fp8 as _fp8
 
 
 class RMSNorm(nn.Module):
@@ -57,24 +66,82 @@ class TuckerMoE(nn.Module):
         self._packed: Optional[torch.Tensor] = None
         self._packed_key = None
         self._warned_grad = False
+        self._fp8: Optional[dict] = None   # e4m3 codes (uint8) and fp32 scales
 
     # -- packed-weight cache -------------------------------------------------
     def _params(self):
         return (self.router.weight, self.U_in, self.inner_norm.weight, self.U_expert,
                 self.core, self.U_out, self.bias)
 
+    def _fp8_tensors(self):
+        f = self._fp8
+        return (f["U_in_q"], f["U_in_scale"], f["core_q"], f["core_scale"], f["U_out_q"],
+                f["U_out_scale"])
+
     def _key(self):
-        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in self._params())
+        ts = self._params() + (self._fp8_tensors() if self._fp8 is not None else ())
+        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in ts)
 
     def plan(self) -> _lib.Plan:
         dtype = self.U_in.dtype
-        if self._plan is None or self._plan.dtype != dtype:
+        fp8 = self._fp8 is not None
+        if self._plan is None or self._plan.dtype != dtype or self._plan.fp8_weights != fp8:
             d_in, r3 = self.U_in.shape
             r2, d_out = self.U_out.shape
             E, r1 = self.U_expert.shape
             self._plan = _lib.Plan(d_in, d_out, E, self.top_k, r1, r2, r3, dtype,
-                                   float(self.inner_norm.eps))
+                                   float(self.inner_norm.eps), fp8_weights=fp8)
         return self._plan
+
+    # -- fp8 weights -----------------------------------------------------------
+    def load_fp8(self, U_in_q, U_in_scale, core_q, core_scale, U_out_q, U_out_scale) -> None:
+        """Loads e4m3 codes (torch.float8_e4m3fn or their uint8 bits) and fp32
+        per-output-channel scales of U_in (d_in, r3) / (r3,), core (r1, r3, r2) /
+        (r1, r2) and U_out (r2, d_out) / (d_out,). The module must be bfloat16."""
+        if self.U_in.dtype != torch.bfloat16:
+            raise RuntimeError(f"TuckerMoE: fp8 weights need a bfloat16 module, not "
+                               f"{self.U_in.dtype}")
+        dev = self.U_in.device
+        shapes = {"U_in": (tuple(self.U_in.shape), (self.U_in.shape[1],)),
+                  "core": (tuple(self.core.shape), (self.core.shape[0], self.core.shape[2])),
+                  "U_out": (tuple(self.U_out.shape), (self.U_out.shape[1],))}
+        given = {"U_in": (U_in_q, U_in_scale), "core": (core_q, core_scale),
+                 "U_out": (U_out_q, U_out_scale)}
+        f = {}
+        for k, (q, sc) in given.items():
+            qs, ss = shapes[k]
+            if q.dtype not in (torch.float8_e4m3fn, torch.uint8):
+                raise RuntimeError(f"TuckerMoE.load_fp8: {k} codes must be float8_e4m3fn or "
+                                   f"uint8, not {q.dtype}")
+            if tuple(q.shape) != qs or tuple(sc.shape) != ss:
+                raise RuntimeError(f"TuckerMoE.load_fp8: {k} codes {tuple(q.shape)} / scales "
+                                   f"{tuple(sc.shape)}, expected {qs} / {ss}")
+            q8 = q.view(torch.uint8) if q.dtype == torch.float8_e4m3fn else q
+            f[f"{k}_q"] = q8.to(dev).contiguous()
+            f[f"{k}_scale"] = sc.to(device=dev, dtype=torch.float32).contiguous()
+        with torch.no_grad():
+            for k, p in (("U_in", self.U_in), ("core", self.core), ("U_out", self.U_out)):
+                p.copy_(_fp8.dequantize(f[f"{k}_q"], f[f"{k}_scale"], k).to(p.dtype))
+        self._fp8 = f
+        self.refresh_packed()
+        self._plan = None
+
+    def quantize_fp8_(self) -> None:
+        """Quantises the current U_in, core and U_out (per-output-channel absmax
+        scaling, fp8.quantize) and loads them with load_fp8()."""
+        q = _fp8.quantize_params({"U_in": self.U_in, "core": self.core, "U_out": self.U_out})
+        self.load_fp8(q["U_in_q"], q["U_in_scale"], q["core_q"], q["core_scale"],
+                      q["U_out_q"], q["U_out_scale"])
+
+    def clear_fp8(self) -> None:
+        """Drops the fp8 weights; the parameters feed the kernels again."""
+        self._fp8 = None
+        self.refresh_packed()
+        self._plan = None
+
+    @property
+    def fp8_weights(self) -> bool:
+        return self._fp8 is not None
 
     def refresh_packed(self) -> None:
         """Forgets the packed copy; the next forward re-packs the parameters."""
@@ -97,15 +164,34 @@ class TuckerMoE(nn.Module):
             buf = torch.empty(plan.packed_bytes(), dtype=torch.uint8, device=dev)
             with torch.cuda.device(dev):
                 stream = torch.cuda.current_stream(dev).cuda_stream
-                _lib.check(_lib.lib().tmoe_pack_weights(
-                    plan.ptr, *[p.data_ptr() for p in params], buf.data_ptr(), stream))
+                if self._fp8 is None:
+                    _lib.check(_lib.lib().tmoe_pack_weights(
+                        plan.ptr, *[p.data_ptr() for p in params], buf.data_ptr(), stream))
+                else:
+                    f = self._fp8
+                    for t in f.values():
+                        if t.device != dev:
+                            raise RuntimeError("TuckerMoE: fp8 weights are on "
+                                               f"{t.device}, parameters on {dev}")
+                    router_w, _, inner_w, U_expert, _, _, bias = params
+                    _lib.check(_lib.lib().tmoe_pack_weights_fp8(
+                        plan.ptr, router_w.data_ptr(), f["U_in_q"].data_ptr(),
+                        f["U_in_scale"].data_ptr(), inner_w.data_ptr(), U_expert.data_ptr(),
+                        f["core_q"].data_ptr(), f["core_scale"].data_ptr(),
+                        f["U_out_q"].data_ptr(), f["U_out_scale"].data_ptr(), bias.data_ptr(),
+                        buf.data_ptr(), stream))
             self._packed, self._packed_key = buf, key
         return self._packed
 
     def _apply(self, fn, *args, **kwargs):
         self.refresh_packed()
         self._plan = None
-        return super()._apply(fn, *args, **kwargs)
+        out = super()._apply(fn, *args, **kwargs)
+        if self._fp8 is not None:
+            # follow the parameters' device; codes and scales keep their dtypes
+            dev = self.U_in.device
+            self._fp8 = {k: v.to(dev) for k, v in self._fp8.items()}
+        return out
 
     # -- forward ---------------------------------------------------------------
     def forward(self, x: torch.Tensor) -> torch.Tensor:

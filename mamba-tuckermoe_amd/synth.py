@@ -21,6 +21,7 @@ from typing import Dict
 import numpy as np
 import torch
 
+from . import fp8
 from .config import Workload
 
 PARAM_KEYS = ("router.weight", "U_in", "inner_norm.weight", "U_expert", "core", "U_out", "bias")
@@ -59,6 +60,27 @@ def make_params(w: Workload, affine: str = "unit", dtype: torch.dtype = None) ->
     else:
         raise ValueError(f"affine={affine!r}: 'unit' or 'random'")
     return {k: round_to(torch.from_numpy(np.ascontiguousarray(p[k])), dtype) for k in PARAM_KEYS}
+
+
+def make_fp8_params(w: Workload, affine: str = "unit"):
+    """fp8-weight variant of make_params (the C5 format).
+
+    The float32 draws of make_params are quantised per output channel (fp8.py):
+    U_in, core and U_out become e4m3 codes + fp32 scales; router.weight,
+    U_expert, inner_norm.weight and bias are rounded to bf16. Returns
+    (params, codes, reference):
+      params     bf16 state_dict for the module (dequantised weights rounded to bf16)
+      codes      {U_in_q, U_in_scale, core_q, core_scale, U_out_q, U_out_scale}
+      reference  float32 state_dict of the layer actually computed: the bf16
+                 values above and the exactly dequantised q * s weights
+    """
+    p32 = make_params(w, affine=affine, dtype=torch.float32)
+    codes = fp8.quantize_params(p32)
+    ref = {k: v.to(torch.bfloat16).float() for k, v in p32.items()}
+    for k in fp8.FP8_KEYS:
+        ref[k] = fp8.dequantize(codes[f"{k}_q"], codes[f"{k}_scale"], k)
+    params = {k: v.to(torch.bfloat16) for k, v in ref.items()}
+    return params, codes, ref
 
 
 def make_x(w: Workload, T: int = None, dtype: torch.dtype = None, stream: int = 0) -> torch.Tensor:

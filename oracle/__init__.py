@@ -11,6 +11,9 @@ Modules:
                     forward, run the way the reference runs it)
   tucker_moe_np     independent float64 numpy formulation (regrouped algebra,
                     argsort top-k) and pure-Python brute force for tiny shapes
+  e4m3              OCP FP8 E4M3 decoding and per-output-channel dequantisation
+                    of the fp8 weight format (the fp8 configuration is the
+                    reference layer on the dequantised weights)
 
 Pinning (tests/test_oracle.py): the two formulations agree with each other and
 with the brute force; the special cases fixed by the mathematics hold (E = k = 1
@@ -18,6 +21,8 @@ dense chain; one-hot U_expert gives per-expert cores; k = 1 scale invariance;
 U_out = 0 gives bias; linearity in core / U_out / bias; softmax weights sum to
 one; token-permutation equivariance; RMSNorm of a constant row; top-k against a
 stable argsort); and planted mistakes in these oracle functions fail at least
-one check. The reference ships no golden vectors for this path
+one check. e4m3 decoding is pinned against torch.float8_e4m3fn on all 256 codes
+and the format's fixed points (zero, smallest subnormal, smallest normal, 448,
+NaN codes). The reference ships no golden vectors for this path
 (pure_torch_mlx has no tests), so no function here is pinned by reference data.
 """

@@ -13,7 +13,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def _header_functions():
     src = open(os.path.join(ROOT, "include", "tmoe.h")).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(tmoe_[a-z_]+)\s*\(", src)))
+    return sorted(set(re.findall(r"\b(tmoe_[a-z0-9_]+)\s*\(", src)))
 
 
 def test_exports_every_header_symbol(pkg):
@@ -116,3 +116,38 @@ def test_plan_wrapper_raises(pkg):
 def test_prof_read_empty(pkg):
     ms, calls = pkg._lib.prof_read()
     assert calls == 0 and ms == [0.0] * pkg._lib.N_STAGES
+
+
+def test_fp8_plan_and_pack_validation(pkg):
+    """TMOE_BF16_FP8W plans: larger packed buffer (the scale arrays), packed only
+    by tmoe_pack_weights_fp8, and every argument error before any HIP call."""
+    L = pkg._lib.lib()
+    rc, p8, _ = _create(pkg, dtype=pkg._lib.TMOE_BF16_FP8W)
+    rc2, pb, _ = _create(pkg, dtype=pkg._lib.TMOE_BF16)
+    assert rc == 0 and rc2 == 0
+    ok = 0x10000
+    try:
+        # + U_in scales (r3), core scale table (r1 * r2), U_out scales (d_out), f32
+        assert L.tmoe_packed_bytes(p8) >= L.tmoe_packed_bytes(pb) + 4 * (128 + 4 * 256 + 1024)
+        assert L.tmoe_workspace_bytes(p8, 64) == L.tmoe_workspace_bytes(pb, 64)
+        pk, pk8 = L.tmoe_pack_weights, L.tmoe_pack_weights_fp8
+        assert pk(p8, ok, ok, ok, ok, ok, ok, ok, ok, None) == -1
+        assert "tmoe_pack_weights_fp8" in L.tmoe_last_error().decode()
+        args = [ok] * 11
+        assert pk8(pb, *args, None) == -1
+        assert "TMOE_BF16_FP8W" in L.tmoe_last_error().decode()
+        for i, name in enumerate(["router_w", "U_in_q", "U_in_scale", "inner_w", "U_expert",
+                                  "core_q", "core_scale", "U_out_q", "U_out_scale", "bias",
+                                  "packed"]):
+            a = list(args)
+            a[i] = None
+            assert pk8(p8, *a, None) == -1, name
+            assert name in L.tmoe_last_error().decode()
+        a = list(args)
+        a[10] = ok + 4
+        assert pk8(p8, *a, None) == -1 and "aligned" in L.tmoe_last_error().decode()
+    finally:
+        L.tmoe_plan_destroy(p8)
+        L.tmoe_plan_destroy(pb)
+    with pytest.raises(pkg._lib.TmoeError):
+        pkg._lib.Plan(512, 1024, 8, 2, 4, 256, 128, torch.float32, 1e-5, fp8_weights=True)

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import e4m3
 from oracle import tucker_moe_np as onp
 from oracle import tucker_moe_torch as ot
 
@@ -156,3 +157,80 @@ def test_side_stream(pkg, dev):
         torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def _fp8_reference(params, codes):
+    """float64 state_dict of the fp8 layer: bf16 router / U_expert / gain / bias
+    and the oracle's dequantisation of the e4m3 weights."""
+    ref = {k: v.double() for k, v in params.items()}
+    for k in ("U_in", "core", "U_out"):
+        q = codes[f"{k}_q"]
+        q = q.view(torch.uint8) if q.dtype == torch.float8_e4m3fn else q
+        ref[k] = torch.from_numpy(e4m3.dequantize(q.numpy(), codes[f"{k}_scale"].double().numpy(), k))
+    return ref
+
+
+def _fp8_module(pkg, dev, w, params, codes):
+    m = _module(pkg, dev, w, params)
+    m.load_fp8(*[codes[k].to(dev) for k in ("U_in_q", "U_in_scale", "core_q", "core_scale",
+                                              "U_out_q", "U_out_scale")])
+    return m
+
+
+@pytest.mark.parametrize("affine", ["unit", "random"])
+def test_fp8_weights_parity(pkg, dev, affine):
+    """C5: e4m3 U_in / core / U_out with per-output-channel scales, against the
+    oracle run on the dequantised weights (bf16 bar)."""
+    w = pkg.WORKLOADS["C5"]
+    params, codes, _ = pkg.synth.make_fp8_params(w, affine=affine)
+    ref = _fp8_reference(params, codes)
+    x = pkg.synth.make_x(w, 1024)
+    got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
+    ref64 = onp.forward_f64(x, ref, w.k)
+    ref32 = {k: v.float() for k, v in ref.items()}
+    tref = ot.forward(x, ref32, w.k, compute_dtype=torch.float32, intermediates=True)
+    _check(w, got, ref64, f"C5/{affine}", tref)
+
+
+def test_fp8_full_size(pkg, dev):
+    w = pkg.WORKLOADS["C5"]
+    params, codes, _ = pkg.synth.make_fp8_params(w)
+    ref = _fp8_reference(params, codes)
+    x = pkg.synth.make_x(w)
+    got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
+    ref64 = onp.forward_f64(x, ref, w.k)
+    ref32 = {k: v.float() for k, v in ref.items()}
+    tref = ot.forward(x[:512], ref32, w.k, compute_dtype=torch.float32, intermediates=True)
+    _check(w, got, ref64, "C5/full", tref)
+
+
+def test_fp8_every_code_and_zero_scales(pkg, dev):
+    """Every finite e4m3 code appears in each weight, with some channels' scales
+    zero (and, for core, a zero scale between non-zero ones of the same column),
+    on a partial last core tile (r2 = 320) and r1 = 3."""
+    w = pkg.Workload("fp8-codes", 300, 256, 192, 8, 2, 3, 128, 320, torch.bfloat16, 91)
+    p32 = pkg.synth.make_params(w, affine="random", dtype=torch.float32)
+    finite = torch.tensor([b for b in range(256) if b not in (0x7F, 0xFF)], dtype=torch.uint8)
+    g = torch.Generator().manual_seed(5)
+
+    def codes_like(shape):
+        n = int(np.prod(shape))
+        return finite[torch.randint(0, len(finite), (n,), generator=g)].reshape(shape)
+
+    codes = {
+        "U_in_q": codes_like((w.d_in, w.r3)),
+        "U_in_scale": torch.rand(w.r3, generator=g) * 0.02,
+        "core_q": codes_like((w.r1, w.r3, w.r2)),
+        "core_scale": torch.rand(w.r1, w.r2, generator=g) * 0.02,
+        "U_out_q": codes_like((w.r2, w.d_out)),
+        "U_out_scale": torch.rand(w.d_out, generator=g) * 0.02,
+    }
+    codes["U_in_scale"][::7] = 0
+    codes["core_scale"][1, ::5] = 0        # rank 1 of every 5th column: 0 between non-zero
+    codes["core_scale"][2, 3::11] = 0      # the last rank
+    codes["U_out_scale"][::13] = 0
+    params = {k: v.to(torch.bfloat16) for k, v in p32.items()}
+    ref = _fp8_reference(params, codes)
+    x = pkg.synth.make_x(w)
+    got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
+    _check(w, got, onp.forward_f64(x, ref, w.k), "fp8 codes/zero scales")

@@ -70,3 +70,61 @@ def test_workload_flops_match_baseline(pkg):
     assert abs(pkg.WORKLOADS["C1"].flops()["total"] / 1e6 - 59.24) < 0.01
     assert abs(pkg.WORKLOADS["C4"].flops()["total"] / 1e9 - 34.36) < 0.01
     assert abs(pkg.WORKLOADS["C3"].hbm_bytes() / 1e6 - 133.49) < 0.05
+
+
+def test_fp8_quantize_per_channel(pkg):
+    """Per-output-channel absmax scales; codes decode (oracle) to within e4m3's
+    half-ulp of w / s; all-zero channels get scale 0 and zero codes."""
+    from oracle import e4m3
+    g = torch.Generator().manual_seed(0)
+    for name, shape, dims in (("U_in", (96, 32), (0,)), ("core", (3, 16, 40), (1,)),
+                              ("U_out", (64, 48), (0,))):
+        w = torch.randn(shape, generator=g) * 0.1
+        if name == "core":
+            w[1, :, 7] = 0
+        else:
+            w[:, 5] = 0
+        q, s = pkg.fp8.quantize(w, name)
+        assert q.dtype == torch.float8_e4m3fn and s.dtype == torch.float32
+        amax = w.abs().amax(dim=dims)
+        assert torch.equal(s, amax / 448.0)
+        v = e4m3.decode(q.view(torch.uint8).numpy())
+        assert not np.isnan(v).any() and np.abs(v).max() <= 448.0
+        s_b = s.unsqueeze(1).numpy() if name == "core" else s.unsqueeze(0).numpy()
+        target = np.where(s_b > 0, w.double().numpy() / np.where(s_b > 0, s_b, 1), 0.0)
+        # e4m3 spacing: 2^(floor(log2|t|) - 3) for normals, 2^-9 below 2^-6
+        ex = np.floor(np.log2(np.maximum(np.abs(target), 2.0 ** -6)))
+        assert (np.abs(v - target) <= 2.0 ** (ex - 4) * (1 + 1e-6)).all()
+        if name == "core":
+            assert s[1, 7] == 0 and (v[1, :, 7] == 0).all()
+        else:
+            assert s[5] == 0 and (v[:, 5] == 0).all()
+        deq = pkg.fp8.dequantize(q, s, name).double().numpy()
+        assert np.allclose(deq, e4m3.dequantize(q.view(torch.uint8).numpy(), s.numpy(), name),
+                           rtol=1e-7, atol=0)
+
+
+def test_fp8_load_validation(pkg):
+    w = pkg.WORKLOADS["C5"].with_T(8)
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(torch.bfloat16)
+    params, codes, _ = pkg.synth.make_fp8_params(w)
+    m.load_state_dict(params)
+    names = ("U_in_q", "U_in_scale", "core_q", "core_scale", "U_out_q", "U_out_scale")
+    args = [codes[k] for k in names]
+    m.load_fp8(*args)
+    assert m.fp8_weights
+    # the parameters now hold the dequantised weights (rounded to bf16)
+    assert torch.equal(m.U_out, params["U_out"])
+    bad = list(args)
+    bad[0] = codes["U_in_q"].float()
+    with pytest.raises(RuntimeError, match="float8_e4m3fn or uint8"):
+        m.load_fp8(*bad)
+    bad = list(args)
+    bad[3] = codes["core_scale"][:, :-1]
+    with pytest.raises(RuntimeError, match="core codes"):
+        m.load_fp8(*bad)
+    m.clear_fp8()
+    assert not m.fp8_weights
+    m32 = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg())
+    with pytest.raises(RuntimeError, match="bfloat16 module"):
+        m32.load_fp8(*args)

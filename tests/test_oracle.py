@@ -241,3 +241,43 @@ def test_planted_mistake_is_caught(name):
 
     res = check_suite(fwd, top_k=2)
     assert any(not ok for _, ok in res), f"mutant '{name}' passed every check"
+
+
+# ---- e4m3 decoding (the fp8 configuration's weight format) --------------------
+
+def test_e4m3_decode_matches_torch_on_every_code():
+    from oracle import e4m3
+    codes = np.arange(256, dtype=np.uint8)
+    ours = e4m3.decode(codes)
+    lib = torch.from_numpy(codes).view(torch.float8_e4m3fn).double().numpy()
+    nan = np.isnan(lib)
+    assert np.array_equal(np.isnan(ours), nan) and nan.sum() == 2
+    assert np.array_equal(ours[~nan], lib[~nan])
+
+
+def test_e4m3_decode_fixed_points():
+    from oracle import e4m3
+    d = e4m3.decode
+    assert d(0x00) == 0.0 and d(0x80) == 0.0 and np.signbit(d(0x80))
+    assert d(0x01) == 2.0 ** -9          # smallest subnormal
+    assert d(0x07) == 7 * 2.0 ** -9      # largest subnormal
+    assert d(0x08) == 2.0 ** -6          # smallest normal
+    assert d(0x38) == 1.0 and d(0xB8) == -1.0
+    assert d(0x7E) == 448.0 and d(0xFE) == -448.0
+    assert np.isnan(d(0x7F)) and np.isnan(d(0xFF))
+
+
+def test_e4m3_dequantize_layouts():
+    from oracle import e4m3
+    g = np.random.default_rng(3)
+    q = g.integers(0, 0x7F, size=(2, 3, 4)).astype(np.uint8)
+    s = g.random((2, 4))
+    w = e4m3.dequantize(q, s, "core")
+    for r in range(2):
+        for t in range(3):
+            for c in range(4):
+                assert w[r, t, c] == e4m3.decode(q[r, t, c]) * s[r, c]
+    q2 = g.integers(0, 0x7F, size=(5, 6)).astype(np.uint8)
+    s2 = g.random(6)
+    w2 = e4m3.dequantize(q2, s2, "U_out")
+    assert np.array_equal(w2, e4m3.decode(q2) * s2[None, :])
