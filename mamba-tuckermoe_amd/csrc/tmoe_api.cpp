@@ -26,7 +26,7 @@ struct tmoe_plan {
   // immediately followed by the router rows (E_pad rows, zero past E). fp8 plans
   // add the U_in column scales, the core scale table and the U_out column scales.
   size_t off_front, off_router, off_gain, off_uexp, off_core, off_uout, off_bias;
-  size_t off_sin, off_cscale, off_sout, packed_bytes;
+  size_t off_sin, off_cscale, off_sout, off_craw, packed_bytes;
 };
 
 namespace {
@@ -72,7 +72,7 @@ hipEvent_t prof_event() {
 }
 
 struct Layout {
-  size_t z, c, idx, w, mid, total;
+  size_t z, c, idx, w, mid, raw, total;
 };
 
 Layout workspace_layout(const tmoe_plan* p, int64_t T) {
@@ -83,6 +83,8 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
   L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
   L.mid = o; o = align256(o + (size_t)T * p->s.r2 * p->es);
+  L.raw = o;
+  if (T <= tmoe::kSmallT) o = align256(o + (size_t)T * (p->s.r3 + p->s.E) * sizeof(float));
   L.total = o;
   return L;
 }
@@ -146,11 +148,12 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   p->off_core = o; o = align256(o + (size_t)s.r2 * s.r1 * s.r3 * p->es);
   p->off_uout = o; o = align256(o + (size_t)s.d_out * s.r2 * p->es);
   p->off_bias = o; o = align256(o + (size_t)s.d_out * sizeof(float));
-  p->off_sin = p->off_cscale = p->off_sout = 0;
+  p->off_sin = p->off_cscale = p->off_sout = p->off_craw = 0;
   if (p->fp8w) {
     p->off_sin = o;    o = align256(o + (size_t)s.r3 * sizeof(float));
     p->off_cscale = o; o = align256(o + (size_t)s.r1 * s.r2 * sizeof(float));
     p->off_sout = o;   o = align256(o + (size_t)s.d_out * sizeof(float));
+    p->off_craw = o;   o = align256(o + (size_t)s.r1 * s.r2 * sizeof(float));
   }
   p->packed_bytes = o;
   *plan_out = p;
@@ -262,6 +265,9 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
   if ((e = tmoe::launch_to_f32(U_out_scale, f32at(p->off_sout), s.d_out, TMOE_F32, st)) !=
       hipSuccess)
     return hip_fail(e, "pack U_out scales");
+  if ((e = tmoe::launch_to_f32(core_scale, f32at(p->off_craw), s.r1 * s.r2, TMOE_F32, st)) !=
+      hipSuccess)
+    return hip_fail(e, "pack core scales");
   return TMOE_OK;
 }
 
@@ -301,6 +307,7 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
     a.zscale = reinterpret_cast<const float*>(pk + p->off_sin);
     a.core_scale = reinterpret_cast<const float*>(pk + p->off_cscale);
     a.out_scale = reinterpret_cast<const float*>(pk + p->off_sout);
+    a.core_scale_raw = reinterpret_cast<const float*>(pk + p->off_craw);
   }
   a.out = out;
   a.idx = topk_idx ? topk_idx : reinterpret_cast<int32_t*>(ws + L.idx);
@@ -309,10 +316,15 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.c = reinterpret_cast<float*>(ws + L.c);
   a.z = ws + L.z;
   a.mid = ws + L.mid;
+  a.raw = reinterpret_cast<float*>(ws + L.raw);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t (*const stages[kStages])(const tmoe::FwdArgs&, hipStream_t) = {
-      tmoe::launch_front, tmoe::launch_core, tmoe::launch_outproj};
+  using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
+  const bool small = T <= tmoe::kSmallT;
+  const Launch big_path[kStages] = {tmoe::launch_front, tmoe::launch_core, tmoe::launch_outproj};
+  const Launch small_path[kStages] = {tmoe::launch_small_front, tmoe::launch_small_core,
+                                      tmoe::launch_small_out};
+  const Launch* stages = small ? small_path : big_path;
   const char* stage_names[kStages] = {"front (router + in-projection)", "core",
                                       "out-projection"};
 

@@ -34,6 +34,7 @@ struct FwdArgs {
   const float* zscale;          // (r3)                 U_in column scales
   const float* core_scale;      // (r1, r2)             rank-change ratios, last rank's scales
   const float* out_scale;       // (d_out)              U_out column scales
+  const float* core_scale_raw;  // (r1, r2)             core channel scales (small-T path)
   // outputs / workspace
   void* out;
   int32_t* idx;                 // (T, k)
@@ -42,12 +43,20 @@ struct FwdArgs {
   float* c;                     // (T, r1)
   void* z;                      // (T, r3)
   void* mid;                    // (T, r2)
+  float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
 };
+
+// Token counts up to kSmallT take the small-T path (tmoe_small.hpp).
+constexpr int64_t kSmallT = 256;
 
 // Each launcher enqueues one kernel on `stream` and returns hipGetLastError().
 hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
+// small-T path: front = skinny GEMM + per-token epilogue; core; out-projection
+hipError_t launch_small_front(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_small_core(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_small_out(const FwdArgs& a, hipStream_t stream);
 
 // Weight packing helpers (stream-ordered).
 // dst(cols, rows) bf16 = e4m3 src(rows, cols)^T; with colscale, entries whose

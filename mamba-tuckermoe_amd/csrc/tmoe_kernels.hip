@@ -1,5 +1,6 @@
 // Launch configurations of the gfx950 kernels (device code: tmoe_kernels.hpp).
 #include "tmoe_kernels.hpp"
+#include "tmoe_small.hpp"
 
 namespace tmoe {
 namespace {
@@ -58,7 +59,59 @@ hipError_t launch_outproj_t(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// small-T path: 16-column work-groups of kSkW waves over blocks of 16 MF tokens
+constexpr int kSkW = 16;
+
+template <int MF, class Elt>
+hipError_t launch_small_front_t(const FwdArgs& a, hipStream_t st) {
+  const dim3 grid(cdiv(a.r3 + a.E, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
+  hipLaunchKernelGGL((dev::k_sk_front<Elt, MF, kSkW>), grid, block, 0, st, a, a.raw);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256), 0, st, a,
+                     (const float*)a.raw);
+  return hipGetLastError();
+}
+
+template <int MF, class Elt>
+hipError_t launch_small_core_t(const FwdArgs& a, hipStream_t st) {
+  const dim3 grid(cdiv(a.r2, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
+  hipLaunchKernelGGL((dev::k_sk_core<Elt, MF, kSkW>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+template <int MF, class Elt>
+hipError_t launch_small_out_t(const FwdArgs& a, hipStream_t st) {
+  const dim3 grid(cdiv(a.d_out, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
+  hipLaunchKernelGGL((dev::k_sk_out<Elt, MF, kSkW>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+// rows per work-group: 16, 32 or 64 tokens
+template <template <int, class> class L>
+hipError_t by_rows(const FwdArgs& a, hipStream_t st) {
+  const bool bf = a.dtype == kDtypeBF16;
+  if (a.T <= 16) return bf ? L<1, EltBF16>::run(a, st) : L<1, EltF32>::run(a, st);
+  if (a.T <= 32) return bf ? L<2, EltBF16>::run(a, st) : L<2, EltF32>::run(a, st);
+  return bf ? L<4, EltBF16>::run(a, st) : L<4, EltF32>::run(a, st);
+}
+template <int MF, class Elt>
+struct SmallFront {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_front_t<MF, Elt>(a, st); }
+};
+template <int MF, class Elt>
+struct SmallCore {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_core_t<MF, Elt>(a, st); }
+};
+template <int MF, class Elt>
+struct SmallOut {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_out_t<MF, Elt>(a, st); }
+};
+
 }  // namespace
+
+hipError_t launch_small_front(const FwdArgs& a, hipStream_t st) { return by_rows<SmallFront>(a, st); }
+hipError_t launch_small_core(const FwdArgs& a, hipStream_t st) { return by_rows<SmallCore>(a, st); }
+hipError_t launch_small_out(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOut>(a, st); }
 
 hipError_t launch_front(const FwdArgs& a, hipStream_t st) {
   return a.dtype == kDtypeBF16 ? launch_front_t<EltBF16>(a, st) : launch_front_t<EltF32>(a, st);

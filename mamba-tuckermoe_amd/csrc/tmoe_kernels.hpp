@@ -571,6 +571,7 @@ __device__ __forceinline__ void flush_tile(const char* stage, T* dst, int64_t ld
 }
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
 
 // ---- k_front: in-projection + RMSNorm, router + top-k + softmax + c --------
 // model.py:75-81 (+ the U_expert gather of :93 folded into c). One work-group:
@@ -585,12 +586,36 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 //  wave order; otherwise the waves split the router columns. Top-k: k rounds
 //  of a wave-wide arg-max over the row's logits: larger logit first, NaN above
 //  every number (torch.topk's order), equal values by lower expert index.
+// Index 0x7fffffff stands for "no candidate" and ranks after every real one.
+// Written as one select expression: no branches in the top-k loops.
 __device__ __forceinline__ bool ranks_before(float v1, int i1, float v2, int i2) {
-  if (i2 == 0x7fffffff) return i1 != 0x7fffffff;
-  if (i1 == 0x7fffffff) return false;
+  const bool none1 = i1 == 0x7fffffff, none2 = i2 == 0x7fffffff;
   const bool n1 = v1 != v1, n2 = v2 != v2;
-  if (n1 || n2) return n1 && (!n2 || i1 < i2);
-  return v1 > v2 || (v1 == v2 && i1 < i2);
+  const bool lower = i1 < i2;
+  const bool num = (v1 > v2) | ((v1 == v2) & lower);
+  const bool nan_rule = n1 & (!n2 | lower);
+  const bool real = (n1 | n2) ? nan_rule : num;
+  return none2 ? !none1 : (!none1 & real);
+}
+
+// Arg-max over aligned groups of G in {1, 2, 4, 8} lanes with DPP moves (VALU
+// cross-lane reads, no LDS traffic): quad_perm [1,0,3,2] and [2,3,0,1] combine
+// lanes at xor 1 and xor 2, row_half_mirror lane i with 7 - i of its 8-lane
+// half row. After the steps every lane of a group holds the group's best.
+template <int CTRL>
+__device__ __forceinline__ void dpp_argmax_step(float& bv, int& bi) {
+  const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), CTRL, 0xf, 0xf, false));
+  const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xf, 0xf, false);
+  const bool b = ranks_before(ov, oi, bv, bi);
+  bv = b ? ov : bv;
+  bi = b ? oi : bi;
+}
+template <int G>
+__device__ __forceinline__ void group_argmax(float& bv, int& bi) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
+  if constexpr (G >= 2) dpp_argmax_step<0xb1>(bv, bi);    // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) dpp_argmax_step<0x4e>(bv, bi);    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) dpp_argmax_step<0x141>(bv, bi);   // row_half_mirror
 }
 
 template <class Elt, int FM, int NR, int NW>
@@ -638,7 +663,9 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
   constexpr int LD = EP + 1;
   constexpr int kPlanes = RX::kSplitK ? NW : 1;
   constexpr int kZBytes = TileStage<TL, T>::kBytes;
-  constexpr int kEpiBytes = kZBytes + (kPlanes * BM * LD + NW * BM) * 4;
+  // + per-row top-k record: exp weights and indices of the k rounds, and their sum
+  constexpr int kEpiBytes =
+      kZBytes + (kPlanes * BM * LD + NW * BM + BM + BM * (2 * kMaxTopK + 1)) * 4;
   // U_expert is staged after that: at least 4 KB (E = 256, r1 = 4) of room
   constexpr int kSmemBytes = cmax(TL::kLdsBytes, kEpiBytes + 4096);
   __shared__ u32x4 smem[kSmemBytes / 16];
@@ -704,6 +731,16 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
       for (int e = 0; e < 16; ++e) red[wave * BM + i * 32 + acc_row(lane, e)] = ss[i][e];
   }
   __syncthreads();
+  // one thread per row: the waves' partial sums in wave order, then 1 / rms
+  float* inv = red + NW * BM;   // [BM]
+  if (threadIdx.x < BM) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += red[w * BM + threadIdx.x];
+    // z / rms as z * (1 / rms): within one fp32 rounding of the division
+    inv[threadIdx.x] = 1.f / sqrtf(tot / (float)R3 + a.eps);
+  }
+  __syncthreads();
 
   // -- z = (z / rms) * g, staged in LDS then written as 16-byte chunks ----------
   {
@@ -716,11 +753,7 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = i * 32 + acc_row(lane, e);
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) tot += red[w * BM + row];
-        // z / rms as z * (1 / rms): within one fp32 rounding of the division
-        const float inv_rms = 1.f / sqrtf(tot / (float)R3 + a.eps);
+        const float inv_rms = inv[row];
 #pragma unroll
         for (int j = 0; j < TL::FN; ++j) {
           const int col = wave * TL::kWaveN + j * 32 + (lane & 31);
@@ -733,27 +766,36 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
   flush_tile<TL, T>(zst, reinterpret_cast<T*>(a.z) + m0 * R3, R3, rows_valid, R3);
 
   // -- top-k, softmax, c -------------------------------------------------------
-  // Each row is resolved by a group of G lanes holding 4 logits each (columns
-  // gl, gl + G, ...), so a wave works on 64 / G rows at once. U_expert is read
-  // from LDS when it fits in the space left after the logits.
-  constexpr int G = EP / 4 < 8 ? 8 : (EP / 4 > 64 ? 64 : EP / 4);
+  // A row is resolved by a group of G lanes (1 to 8; as many as fill the
+  // work-group, and at least EP / 32) holding EP / G <= 32 logits each (columns
+  // gl, gl + G, ...): K rounds of a serial arg-max over the lane's logits and a
+  // DPP arg-max over the group, with no LDS traffic in the rounds. Round kk's
+  // exp(v - v_max) and index go to LDS; then the softmax weights and c are
+  // formed in parallel over (row, round) and (row, r). U_expert is read from
+  // LDS when it fits in the space left after the logits.
+  constexpr int kFill = 64 * NW / BM;
+  constexpr int G = cmin(8, cmax(EP / 32, kFill < 1 ? 1 : kFill));
   constexpr int PL = EP / G;          // logits per lane
+  static_assert(PL <= 32 && EP % G == 0, "taken-mask width");
   constexpr int RPW = 64 / G;         // rows per wave per pass
   constexpr int kUeBytes = kSmemBytes - kEpiBytes;
   const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
+  float* rec_ex = inv + BM;                       // [BM][kMaxTopK]
+  int* rec_i = reinterpret_cast<int*>(rec_ex + BM * kMaxTopK);   // [BM][kMaxTopK]
+  float* rec_sum = reinterpret_cast<float*>(rec_i + BM * kMaxTopK);   // [BM]
+  float* ue = rec_sum + BM;
   const bool ue_lds = E * R1 * 4 <= kUeBytes;
-  float* ue = red + NW * BM;
   if (ue_lds)
     for (int i = threadIdx.x; i < E * R1; i += TL::kThreads) ue[i] = a.uexp[i];
-  __syncthreads();
   const float* uex = ue_lds ? ue : a.uexp;
   const int gl = lane % G;
   for (int row0 = wave * RPW; row0 < BM; row0 += NW * RPW) {
-    const int row = row0 + lane / G;
-    const bool live = row < rows_valid;
+    const int row_raw = row0 + lane / G;
+    const bool inb = row_raw < BM;
+    const int row = inb ? row_raw : BM - 1;   // lanes past the tile repeat its last row
+    const bool live = inb && row < rows_valid;
     const int64_t g = m0 + row;
     float v[PL];
-    unsigned taken = 0;
 #pragma unroll
     for (int p = 0; p < PL; ++p) {
       const int col = gl + G * p;
@@ -767,67 +809,46 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
       v[p] = sc;
       if (a.logits && live && col < E) a.logits[g * E + col] = sc;
     }
-    float sel_v[kMaxTopK];
-    int sel_i[kMaxTopK];
+    unsigned taken = 0;
+    float vmax = 0.f, ssum = 0.f;
+#pragma unroll 1
+    for (int kk = 0; kk < K; ++kk) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;   // "no candidate": loses to every real one
 #pragma unroll
-    for (int kk = 0; kk < kMaxTopK; ++kk) {
-      sel_v[kk] = 0.f;
-      sel_i[kk] = 0;
-      if (kk < K) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;   // "no candidate": loses to every real one
-#pragma unroll
-        for (int p = 0; p < PL; ++p) {
-          const int col = gl + G * p;
-          const bool ok = col < E && !((taken >> p) & 1u);
-          if (ok && ranks_before(v[p], col, bv, bi)) {
-            bv = v[p];
-            bi = col;
-          }
-        }
-#pragma unroll
-        for (int off = G / 2; off >= 1; off >>= 1) {   // stays inside the group
-          const float ov = __shfl_xor(bv, off);
-          const int oi = __shfl_xor(bi, off);
-          if (ranks_before(ov, oi, bv, bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
-        // k <= E, so a candidate always remains and bi < E here.
-        if (bi % G == gl) taken |= 1u << (bi / G);
-        sel_v[kk] = bv;
-        sel_i[kk] = bi;
+      for (int p = 0; p < PL; ++p) {
+        const int col = gl + G * p;
+        const bool ok = (col < E) & !((taken >> p) & 1u) & ranks_before(v[p], col, bv, bi);
+        bv = ok ? v[p] : bv;
+        bi = ok ? col : bi;
+      }
+      group_argmax<G>(bv, bi);
+      // k <= E, so a candidate always remains and bi < E here.
+      if (bi % G == gl) taken |= 1u << (bi / G);
+      if (kk == 0) vmax = bv;   // the largest
+      const float ex = expf(bv - vmax);
+      ssum += ex;
+      if (gl == 0 && inb) {
+        rec_ex[row * kMaxTopK + kk] = ex;
+        rec_i[row * kMaxTopK + kk] = bi;
       }
     }
-    // softmax over the selected logits (sel_v[0] is the largest)
-    float ex[kMaxTopK];
-    float ssum = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < kMaxTopK; ++kk) {
-      ex[kk] = 0.f;
-      if (kk < K) {
-        ex[kk] = expf(sel_v[kk] - sel_v[0]);
-        ssum += ex[kk];
-      }
-    }
-    if (live) {
-#pragma unroll
-      for (int kk = 0; kk < kMaxTopK; ++kk) {
-        if (kk < K && kk % G == gl) {
-          a.idx[g * K + kk] = sel_i[kk];
-          a.w[g * K + kk] = ex[kk] / ssum;
-        }
-      }
-      // c[r] = sum_j w_j * U_expert[e_j, r]
-      for (int r = gl; r < R1; r += G) {
-        float cr = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < kMaxTopK; ++kk)
-          if (kk < K) cr += (ex[kk] / ssum) * uex[sel_i[kk] * R1 + r];
-        a.c[g * R1 + r] = cr;
-      }
-    }
+    if (gl == 0 && inb) rec_sum[row] = ssum;
+  }
+  __syncthreads();
+  // softmax weights (model.py:77) and c = sum_j w_j U_expert[e_j] (model.py:93)
+  for (int q = threadIdx.x; q < rows_valid * K; q += TL::kThreads) {
+    const int row = q / K, kk = q - row * K;
+    a.idx[(m0 + row) * K + kk] = rec_i[row * kMaxTopK + kk];
+    a.w[(m0 + row) * K + kk] = rec_ex[row * kMaxTopK + kk] / rec_sum[row];
+  }
+  for (int q = threadIdx.x; q < rows_valid * R1; q += TL::kThreads) {
+    const int row = q / R1, r = q - row * R1;
+    const float sum = rec_sum[row];
+    float cr = 0.f;
+    for (int kk = 0; kk < K; ++kk)
+      cr += (rec_ex[row * kMaxTopK + kk] / sum) * uex[rec_i[row * kMaxTopK + kk] * R1 + r];
+    a.c[(m0 + row) * R1 + r] = cr;
   }
 }
 

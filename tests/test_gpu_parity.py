@@ -100,11 +100,13 @@ SHAPES = [
 ]
 
 
+# T = 200 takes the small-T kernels, T = 600 the large-tile ones
+@pytest.mark.parametrize("T", [200, 600])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "E%d_k%d_r%d-%d-%d_%dx%d" % s)
-def test_shapes(pkg, dev, shape, dtype):
+def test_shapes(pkg, dev, shape, dtype, T):
     E, k, r1, r3, r2, d_in, d_out = shape
-    w = pkg.Workload("custom", 200, d_in, d_out, E, k, r1, r3, r2, dtype, 77)
+    w = pkg.Workload("custom", T, d_in, d_out, E, k, r1, r3, r2, dtype, 77)
     params = pkg.synth.make_params(w, affine="random")
     x = pkg.synth.make_x(w)
     got = _run(_module(pkg, dev, w, params), x, dev)
@@ -192,6 +194,16 @@ def test_fp8_weights_parity(pkg, dev, affine):
     _check(w, got, ref64, f"C5/{affine}", tref)
 
 
+def test_fp8_decode(pkg, dev):
+    """C5's shapes at a decode-sized batch (small-T kernels)."""
+    w = pkg.WORKLOADS["C5"].with_T(32)
+    params, codes, _ = pkg.synth.make_fp8_params(w, affine="random")
+    ref = _fp8_reference(params, codes)
+    x = pkg.synth.make_x(w)
+    got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
+    _check(w, got, onp.forward_f64(x, ref, w.k), "C5/T=32")
+
+
 def test_fp8_full_size(pkg, dev):
     w = pkg.WORKLOADS["C5"]
     params, codes, _ = pkg.synth.make_fp8_params(w)
@@ -204,11 +216,13 @@ def test_fp8_full_size(pkg, dev):
     _check(w, got, ref64, "C5/full", tref)
 
 
-def test_fp8_every_code_and_zero_scales(pkg, dev):
+@pytest.mark.parametrize("T", [40, 300])
+def test_fp8_every_code_and_zero_scales(pkg, dev, T):
     """Every finite e4m3 code appears in each weight, with some channels' scales
     zero (and, for core, a zero scale between non-zero ones of the same column),
-    on a partial last core tile (r2 = 320) and r1 = 3."""
-    w = pkg.Workload("fp8-codes", 300, 256, 192, 8, 2, 3, 128, 320, torch.bfloat16, 91)
+    on a partial last core tile (r2 = 320) and r1 = 3; T = 40 takes the small-T
+    kernels, T = 300 the large-tile ones."""
+    w = pkg.Workload("fp8-codes", T, 256, 192, 8, 2, 3, 128, 320, torch.bfloat16, 91)
     p32 = pkg.synth.make_params(w, affine="random", dtype=torch.float32)
     finite = torch.tensor([b for b in range(256) if b not in (0x7F, 0xFF)], dtype=torch.uint8)
     g = torch.Generator().manual_seed(5)
