@@ -23,7 +23,7 @@ struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 
 template <class Elt, int R3>
 hipError_t launch_front_r3(const FwdArgs& a, hipStream_t st) {
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-  const dim3 grid(cdiv(a.T, kFrontBM)), block(64 * NW);
+  const dim3 grid(cdiv(a.T, kFrontBM)), block(64 * NW * kFrontWM);
   switch (a.E_pad / 32) {
     case 1: hipLaunchKernelGGL((dev::k_front<Elt, R3, 1>), grid, block, 0, st, a); break;
     case 2: hipLaunchKernelGGL((dev::k_front<Elt, R3, 2>), grid, block, 0, st, a); break;

@@ -221,6 +221,8 @@ __device__ __forceinline__ int dma_chunk(int lane, int blk) {
 
 // A main-loop consumer: operator() runs after every K step's MFMAs with that
 // step's A fragments; tile_begin(kt, acc) runs before the MFMAs of K tile kt.
+__device__ __forceinline__ int cmin_dev(int a, int b) { return a < b ? a : b; }
+
 struct NoExtra {
   template <class AF>
   __device__ __forceinline__ void operator()(const u32x4*, int, int, const AF&) const {}
@@ -239,10 +241,13 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
   constexpr int W = TL::kThreads / 64;
   constexpr int kARows = TL::BM, kBRows = TL::kBRows;
   constexpr int AP = ADMA ? 0 : TL::kAPerThread, BP = BDMA ? 0 : TL::kBPerThread;
-  // DMA instructions each wave issues per tile
-  constexpr int ADN = ADMA ? kARows / 8 / W : 0, BDN = BDMA ? kBRows / 8 / W : 0;
-  static_assert(!ADMA || (kARows / 8) % W == 0, "A DMA blocks must split evenly over waves");
-  static_assert(!BDMA || (kBRows / 8) % W == 0, "B DMA blocks must split evenly over waves");
+  // DMA instructions each wave issues per tile. When the 8-row blocks do not
+  // split evenly over the waves, the extra slots repeat the last block: the same
+  // bytes to the same LDS slots, waited for like any other, so every wave issues
+  // the same count and one vmcnt bound holds for all.
+  constexpr int kANBlk = kARows / 8, kBNBlk = kBRows / 8;
+  constexpr int ADN = ADMA ? (kANBlk + W - 1) / W : 0, BDN = BDMA ? (kBNBlk + W - 1) / W : 0;
+  static_assert(kARows % 16 == 0 && kBRows % 8 == 0, "DMA blocks of 8 rows");
   // every thread issues the same loads, so one vmcnt count holds for all waves
   static_assert(ADMA || AP * TL::kThreads == kARows * CH, "register-staged A: full rounds");
   static_assert(BDMA || BP * TL::kThreads == kBRows * CH, "register-staged B: full rounds");
@@ -293,7 +298,7 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
     u32x4* s = smem + stage * TL::kStage;
     if (j < ADN) {
       if constexpr (ADMA) {
-        const int blk = wave + j * W;
+        const int blk = cmin_dev(wave + j * W, kANBlk - 1);
         __builtin_amdgcn_global_load_lds(
             (gbl_cvptr)aload.gaddr(blk * 8 + (lane >> 3), dma_chunk(lane, blk), kt),
             (lds_vptr)(s + blk * 64), 16, 0, 0);
@@ -302,7 +307,7 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
       if constexpr (BDMA) {
         // kARows is a multiple of 16, so the block parity within B equals the
         // parity of its LDS block
-        const int blk = wave + (j - ADN) * W;
+        const int blk = cmin_dev(wave + (j - ADN) * W, kBNBlk - 1);
         __builtin_amdgcn_global_load_lds(
             (gbl_cvptr)bload.gaddr(blk * 8 + (lane >> 3), dma_chunk(lane, blk), kt),
             (lds_vptr)(s + (kARows + blk * 8) * 8), 16, 0, 0);
@@ -576,46 +581,53 @@ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 // ---- k_front: in-projection + RMSNorm, router + top-k + softmax + c --------
 // model.py:75-81 (+ the U_expert gather of :93 folded into c). One work-group:
 // BM tokens x (R3 z columns + EP router columns), NW = R3 / 32 (at most 4) waves
-// side by side over the z columns, each owning all BM rows. BM = 32 keeps the
-// LDS under 80 KB, so two work-groups share a CU and one's epilogue overlaps
-// the other's main loop.
+// side by side over the z columns in each of WMF row groups (a wave owns BM / WMF
+// rows). The row groups share the weight stages in LDS. With BM = 32 and one
+// row group the LDS stays under 80 KB, so two work-groups share a CU and one's
+// epilogue overlaps the other's main loop.
 //  z part: epilogue z = (z / rms) * g with rms = sqrt(mean(z^2) + eps)
 //  (model.py:25-27), the division taken as a multiply by 1 / rms.
 //  router part (NR = EP/32 column blocks): with NR < NW every wave computes all
-//  router columns over every NW-th K step and the partial sums are added in
-//  wave order; otherwise the waves split the router columns. Top-k: k rounds
-//  of a wave-wide arg-max over the row's logits: larger logit first, NaN above
-//  every number (torch.topk's order), equal values by lower expert index.
-// Index 0x7fffffff stands for "no candidate" and ranks after every real one.
-// Written as one select expression: no branches in the top-k loops.
-__device__ __forceinline__ bool ranks_before(float v1, int i1, float v2, int i2) {
-  const bool none1 = i1 == 0x7fffffff, none2 = i2 == 0x7fffffff;
-  const bool n1 = v1 != v1, n2 = v2 != v2;
-  const bool lower = i1 < i2;
-  const bool num = (v1 > v2) | ((v1 == v2) & lower);
-  const bool nan_rule = n1 & (!n2 | lower);
-  const bool real = (n1 | n2) ? nan_rule : num;
-  return none2 ? !none1 : (!none1 & real);
+//  router columns of its rows over every NW-th K step and the partial sums are
+//  added in wave order; otherwise the waves split the router columns. Top-k:
+//  k rounds of a max over rank_key (torch.topk's order) within a group of lanes
+//  per row.
+// Top-k order (torch.topk, model.py:76): larger logit first, NaN above every
+// number, equal values by lower expert index. As one unsigned 64-bit key,
+// larger = ranks first: high word the logit mapped to an order-preserving
+// unsigned integer (-0 canonicalised to +0 so that it ties with +0; every NaN
+// mapped to the top), low word ~index (a lower index wins a tie). Key 0 is below
+// every candidate and stands for "none".
+__device__ __forceinline__ uint64_t rank_key(float v, int idx) {
+  const float c = v + 0.f;   // -0 + 0 = +0 (round to nearest)
+  const uint32_t u = __float_as_uint(c);
+  uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  k = (c != c) ? 0xffffffffu : k;
+  return ((uint64_t)k << 32) | (uint32_t)~(uint32_t)idx;
+}
+__device__ __forceinline__ int key_index(uint64_t key) { return (int)~(uint32_t)key; }
+__device__ __forceinline__ float key_value(uint64_t key) {   // the canonical logit
+  const uint32_t k = (uint32_t)(key >> 32);
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Arg-max over aligned groups of G in {1, 2, 4, 8} lanes with DPP moves (VALU
+// Max-key over aligned groups of G in {1, 2, 4, 8} lanes with DPP moves (VALU
 // cross-lane reads, no LDS traffic): quad_perm [1,0,3,2] and [2,3,0,1] combine
 // lanes at xor 1 and xor 2, row_half_mirror lane i with 7 - i of its 8-lane
 // half row. After the steps every lane of a group holds the group's best.
 template <int CTRL>
-__device__ __forceinline__ void dpp_argmax_step(float& bv, int& bi) {
-  const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), CTRL, 0xf, 0xf, false));
-  const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xf, 0xf, false);
-  const bool b = ranks_before(ov, oi, bv, bi);
-  bv = b ? ov : bv;
-  bi = b ? oi : bi;
+__device__ __forceinline__ void dpp_max_step(uint64_t& key) {
+  const uint32_t lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)key, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(key >> 32), CTRL, 0xf, 0xf, false);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  key = o > key ? o : key;
 }
 template <int G>
-__device__ __forceinline__ void group_argmax(float& bv, int& bi) {
+__device__ __forceinline__ void group_max_key(uint64_t& key) {
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
-  if constexpr (G >= 2) dpp_argmax_step<0xb1>(bv, bi);    // quad_perm [1,0,3,2]
-  if constexpr (G >= 4) dpp_argmax_step<0x4e>(bv, bi);    // quad_perm [2,3,0,1]
-  if constexpr (G >= 8) dpp_argmax_step<0x141>(bv, bi);   // row_half_mirror
+  if constexpr (G >= 2) dpp_max_step<0xb1>(key);    // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) dpp_max_step<0x4e>(key);    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) dpp_max_step<0x141>(key);   // row_half_mirror
 }
 
 template <class Elt, int FM, int NR, int NW>
@@ -649,15 +661,17 @@ struct RouterExtra {
   __device__ __forceinline__ void tile_begin(int, ACC&) const {}
 };
 
-template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2>
-__global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
+          int WMF = kFrontWM>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
   typedef typename Elt::T T;
   constexpr int EP = 32 * NR;
-  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-  // x streams from HBM once: a register ring holds PFA of its K tiles (two
-  // chunks per thread each). The weight rows come from L2 by DMA into LDS.
-  typedef Tile<BM, R3, EP, 1, NW, PFA, 1, NS, false, true> TL;
-  constexpr int FM = TL::FM;   // every wave covers all BM rows
+  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;   // waves across the z columns
+  constexpr int NWT = NW * WMF;                      // all waves (WMF row groups)
+  // x streams from HBM once: a register ring holds PFA of its K tiles. The
+  // weight rows come from L2 by DMA into LDS, shared by the WMF row groups.
+  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true> TL;
+  constexpr int FM = TL::FM;   // a wave covers the BM / WMF rows of its group
   typedef RouterExtra<Elt, FM, NR, NW> RX;
   // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
   constexpr int LD = EP + 1;
@@ -671,6 +685,7 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
   __shared__ u32x4 smem[kSmemBytes / 16];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;   // column wave, first row
   const int64_t m0 = (int64_t)blockIdx.x * BM;
   const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
   const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
@@ -678,7 +693,7 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
   RowLoader bl{reinterpret_cast<const char*>(a.wfront), row_bytes, R3 + EP};
   f32x16 acc[FM][TL::FN];
   RX rx;
-  rx.init(wave, lane, BM + R3);
+  rx.init(wn, lane, BM + R3);
   gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, rx);
 
   // -- router logits -> LDS, [BM][EP + 1] (split-K: one partial plane per wave) --
@@ -691,18 +706,18 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
     for (int j = 0; j < RX::RT; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int row = i * 32 + acc_row(lane, e);
+        const int row = wrow + i * 32 + acc_row(lane, e);
         if constexpr (RX::kSplitK)
-          lg[(wave * BM + row) * LD + j * 32 + (lane & 31)] = rx.racc[i][j][e];
+          lg[(wn * BM + row) * LD + j * 32 + (lane & 31)] = rx.racc[i][j][e];
         else
-          lg[row * LD + (wave * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
+          lg[row * LD + (wn * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
       }
 
   // -- fp8 weights: z column j = (x . q_in[:, j]) * s_in[j] ----------------
   if (a.zscale) {
 #pragma unroll
     for (int j = 0; j < TL::FN; ++j) {
-      const float sc = a.zscale[wave * TL::kWaveN + j * 32 + (lane & 31)];
+      const float sc = a.zscale[wn * TL::kWaveN + j * 32 + (lane & 31)];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -728,7 +743,7 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) red[wave * BM + i * 32 + acc_row(lane, e)] = ss[i][e];
+      for (int e = 0; e < 16; ++e) red[wn * BM + wrow + i * 32 + acc_row(lane, e)] = ss[i][e];
   }
   __syncthreads();
   // one thread per row: the waves' partial sums in wave order, then 1 / rms
@@ -747,16 +762,16 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
     constexpr int RB = TileStage<TL, T>::kRowBytes;
     float gcol[TL::FN];
 #pragma unroll
-    for (int j = 0; j < TL::FN; ++j) gcol[j] = a.gain[wave * TL::kWaveN + j * 32 + (lane & 31)];
+    for (int j = 0; j < TL::FN; ++j) gcol[j] = a.gain[wn * TL::kWaveN + j * 32 + (lane & 31)];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int row = i * 32 + acc_row(lane, e);
+        const int row = wrow + i * 32 + acc_row(lane, e);
         const float inv_rms = inv[row];
 #pragma unroll
         for (int j = 0; j < TL::FN; ++j) {
-          const int col = wave * TL::kWaveN + j * 32 + (lane & 31);
+          const int col = wn * TL::kWaveN + j * 32 + (lane & 31);
           store_from_f32(reinterpret_cast<T*>(zst + row * RB + col * (int)sizeof(T)),
                          (acc[i][j][e] * inv_rms) * gcol[j]);
         }
@@ -773,7 +788,7 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
   // exp(v - v_max) and index go to LDS; then the softmax weights and c are
   // formed in parallel over (row, round) and (row, r). U_expert is read from
   // LDS when it fits in the space left after the logits.
-  constexpr int kFill = 64 * NW / BM;
+  constexpr int kFill = 64 * NWT / BM;
   constexpr int G = cmin(8, cmax(EP / 32, kFill < 1 ? 1 : kFill));
   constexpr int PL = EP / G;          // logits per lane
   static_assert(PL <= 32 && EP % G == 0, "taken-mask width");
@@ -789,13 +804,13 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
     for (int i = threadIdx.x; i < E * R1; i += TL::kThreads) ue[i] = a.uexp[i];
   const float* uex = ue_lds ? ue : a.uexp;
   const int gl = lane % G;
-  for (int row0 = wave * RPW; row0 < BM; row0 += NW * RPW) {
+  for (int row0 = wave * RPW; row0 < BM; row0 += NWT * RPW) {
     const int row_raw = row0 + lane / G;
     const bool inb = row_raw < BM;
     const int row = inb ? row_raw : BM - 1;   // lanes past the tile repeat its last row
     const bool live = inb && row < rows_valid;
     const int64_t g = m0 + row;
-    float v[PL];
+    uint64_t key[PL];   // 0 for columns past E and for taken candidates
 #pragma unroll
     for (int p = 0; p < PL; ++p) {
       const int col = gl + G * p;
@@ -806,25 +821,21 @@ __global__ __launch_bounds__(64 * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdA
       } else {
         sc = lg[row * LD + col];
       }
-      v[p] = sc;
+      key[p] = col < E ? rank_key(sc, col) : 0;
       if (a.logits && live && col < E) a.logits[g * E + col] = sc;
     }
-    unsigned taken = 0;
     float vmax = 0.f, ssum = 0.f;
 #pragma unroll 1
     for (int kk = 0; kk < K; ++kk) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;   // "no candidate": loses to every real one
+      uint64_t best = 0;
 #pragma unroll
-      for (int p = 0; p < PL; ++p) {
-        const int col = gl + G * p;
-        const bool ok = (col < E) & !((taken >> p) & 1u) & ranks_before(v[p], col, bv, bi);
-        bv = ok ? v[p] : bv;
-        bi = ok ? col : bi;
-      }
-      group_argmax<G>(bv, bi);
-      // k <= E, so a candidate always remains and bi < E here.
-      if (bi % G == gl) taken |= 1u << (bi / G);
+      for (int p = 0; p < PL; ++p) best = key[p] > best ? key[p] : best;
+      group_max_key<G>(best);
+      // k <= E, so a candidate always remains: best > 0 and its index is < E
+      const int bi = key_index(best);
+      const float bv = key_value(best);
+#pragma unroll
+      for (int p = 0; p < PL; ++p) key[p] = key[p] == best ? 0 : key[p];
       if (kk == 0) vmax = bv;   // the largest
       const float ex = expf(bv - vmax);
       ssum += ex;

@@ -197,7 +197,7 @@ __global__ __launch_bounds__(64 * W) void k_sk_front(FwdArgs a, float* raw) {
 }
 
 // One wave per token: z = RMSNorm(raw z (* U_in scales)) * gain; logits; top-k
-// (the rule of k_front: larger first, NaN above numbers, lower index on ties);
+// (rank_key order: larger first, NaN above numbers, lower index on ties);
 // softmax over the selected; c = sum_j w_j U_expert[e_j].
 template <class Elt>
 __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) {
@@ -233,40 +233,34 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) 
     if (j < R3)
       store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, (zv[q] * inv_rms) * a.gain[j]);
   }
-  float lv[4];
+  uint64_t key[4];   // rank_key order; 0 past E and once taken
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = lane + 64 * q;
-    lv[q] = e < E ? row[R3 + e] : 0.f;
-    if (a.logits && e < E) a.logits[t * E + e] = lv[q];
+    const float lv = e < E ? row[R3 + e] : 0.f;
+    key[q] = e < E ? rank_key(lv, e) : 0;
+    if (a.logits && e < E) a.logits[t * E + e] = lv;
   }
-  // K rounds of a wave arg-max; lane kk keeps round kk's winner (K <= 16 < 64)
-  unsigned taken = 0;
+  // K rounds of a wave max-key; lane kk keeps round kk's winner (K <= 16 < 64)
   float sv = 0.f;
   int si = 0;
 #pragma unroll 1
   for (int kk = 0; kk < K; ++kk) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    uint64_t best = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = lane + 64 * q;
-      const bool ok = (e < E) & !((taken >> q) & 1u) & ranks_before(lv[q], e, bv, bi);
-      bv = ok ? lv[q] : bv;
-      bi = ok ? e : bi;
-    }
+    for (int q = 0; q < 4; ++q) best = key[q] > best ? key[q] : best;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      const bool b = ranks_before(ov, oi, bv, bi);
-      bv = b ? ov : bv;
-      bi = b ? oi : bi;
+      const uint32_t lo = __shfl_xor((uint32_t)best, off);
+      const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off);
+      const uint64_t o = ((uint64_t)hi << 32) | lo;
+      best = o > best ? o : best;
     }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);   // k <= E: bi < E
-    if (kk == lane) {
-      sv = bv;
-      si = bi;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) key[q] = key[q] == best ? 0 : key[q];
+    if (kk == lane) {   // k <= E: best names a candidate, index < E
+      sv = key_value(best);
+      si = key_index(best);
     }
   }
   const float vmax = __shfl(sv, 0);

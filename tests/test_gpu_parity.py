@@ -248,3 +248,26 @@ def test_fp8_every_code_and_zero_scales(pkg, dev, T):
     x = pkg.synth.make_x(w)
     got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
     _check(w, got, onp.forward_f64(x, ref, w.k), "fp8 codes/zero scales")
+
+
+@pytest.mark.parametrize("T", [40, 600])
+@pytest.mark.parametrize("E,k", [(16, 2), (256, 8)])
+def test_exact_ties_pick_lower_index(pkg, dev, T, E, k):
+    """Duplicated router rows give exactly equal logits; zero router rows give
+    +0 and -0 logits for positive / negative x. The lower expert index must
+    win (the oracle's stable argsort); T = 40 / 600 take the small-T / large-tile
+    kernels."""
+    w = pkg.Workload("ties", T, 512, 256, E, k, 4, 128, 256, torch.bfloat16, 123)
+    params = pkg.synth.make_params(w, affine="random")
+    rw = params["router.weight"].clone()
+    for dst, src in ((3, 1), (5, 1), (9, 7), (E - 1, 0)):
+        rw[dst] = rw[src]
+    rw[E - 2] = 0
+    rw[E - 3] = 0
+    params["router.weight"] = rw
+    x = pkg.synth.make_x(w)
+    got = _run(_module(pkg, dev, w, params), x, dev)
+    ref64 = onp.forward_f64(x, params, w.k)
+    idx = got[1].numpy()
+    assert np.array_equal(idx, ref64["idx"][:T]), np.nonzero((idx != ref64["idx"][:T]).any(1))[0][:8]
+    assert onp.rel_l2(got[0].numpy(), ref64["out"][:T]) <= TOL[w.dtype]
