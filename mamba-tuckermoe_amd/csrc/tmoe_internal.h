@@ -11,9 +11,9 @@ namespace tmoe {
 // the kernels. K-direction tiles are 128 bytes of one operand row: 64 bf16 or
 // 32 f32 elements.
 constexpr int kTileKBytes = 128;
-constexpr int kFrontBM = 32;    // tokens per k_front work-group (whole r3 and E rows)
+constexpr int kFrontBM = 64;    // tokens per k_front work-group (whole r3 and E rows)
 constexpr int kFrontPFA = 2;    // K tiles of x in flight per k_front work-group
-constexpr int kFrontWM = 1;     // row groups of waves per k_front work-group
+constexpr int kFrontWM = 2;     // row groups of waves per k_front work-group
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 256;
 

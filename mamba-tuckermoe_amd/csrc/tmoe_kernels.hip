@@ -20,18 +20,26 @@ struct OutCfgBF16 { static constexpr int BM = 256, BN = 192, WM = 4, WN = 2, P =
 struct CoreCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 2; };
 struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 2; };
 
+// Front tiles: kFrontBM tokens in kFrontWM row groups; with the widest router
+// (E > 128) one group of 32 tokens, whose smaller LDS footprint measured faster.
+template <class Elt, int R3, int NR>
+hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
+  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
+  constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
+  const dim3 grid(cdiv(a.T, BM)), block(64 * NW * WM);
+  hipLaunchKernelGGL((dev::k_front<Elt, R3, NR, kFrontPFA, BM, 2, WM>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 template <class Elt, int R3>
 hipError_t launch_front_r3(const FwdArgs& a, hipStream_t st) {
-  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-  const dim3 grid(cdiv(a.T, kFrontBM)), block(64 * NW * kFrontWM);
   switch (a.E_pad / 32) {
-    case 1: hipLaunchKernelGGL((dev::k_front<Elt, R3, 1>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((dev::k_front<Elt, R3, 2>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((dev::k_front<Elt, R3, 4>), grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL((dev::k_front<Elt, R3, 8>), grid, block, 0, st, a); break;
+    case 1: return launch_front_nr<Elt, R3, 1>(a, st);
+    case 2: return launch_front_nr<Elt, R3, 2>(a, st);
+    case 4: return launch_front_nr<Elt, R3, 4>(a, st);
+    case 8: return launch_front_nr<Elt, R3, 8>(a, st);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 template <class Elt>
