@@ -29,6 +29,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "TuckerMoE layer tokens/sec + % bf16 MFMA peak at T=16384; vs host-CPU ref"
 PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}   # MI355X dense MFMA
+HBM_PEAK_GBS = 8000.0                            # MI355X HBM3E
 PEAK_HBM_GBS = 8000.0
 
 
@@ -175,12 +176,18 @@ def main():
     stage_avg_us = {n: stage_ms[j] / calls * 1e3 for j, n in enumerate(pkg._lib.STAGE_NAMES)}
     fl = w.flops()
     fl["front"] = fl["router"] + fl["in_proj"]   # one kernel computes both
+    sb = w.stage_bytes()
     dom = max(stage_avg_us, key=stage_avg_us.get)
     dom_tflops = fl[dom] / (stage_avg_us[dom] * 1e-6) / 1e12
+    dom_gbs = sb[dom] / (stage_avg_us[dom] * 1e-6) / 1e9
     peak = PEAK_TFLOPS[dt_name]
+    # the bound of the dominant kernel: MFMA when its arithmetic intensity is above
+    # the ridge (peak flop/s over HBM bytes/s), HBM otherwise
+    mfma_bound = fl[dom] / sb[dom] >= peak * 1e12 / (HBM_PEAK_GBS * 1e9)
     layer_tflops = fl["total"] / (ms_per_step * 1e-3) / 1e12
     log("[bench] per-stage avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in stage_avg_us.items()))
-    log(f"[bench] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak; "
+    log(f"[bench] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak, "
+        f"{dom_gbs:.1f} GB/s = {dom_gbs / HBM_PEAK_GBS:.3f} of HBM; "
         f"layer {layer_tflops:.1f} TFLOP/s = {layer_tflops / peak:.3f} of peak")
 
     if args.copy_calibration_mib:
@@ -257,9 +264,13 @@ def main():
                    "r1": w.r1, "r3": w.r3, "r2": w.r2, "rotated_sets": n_sets,
                    "weights": ("U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales, "
                                "unpacked exactly to bf16; bf16 MFMA" if w.fp8 else dt_name)},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,
-                     "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
-                     "avg_us": stage_avg_us[dom], "flops_per_launch": fl[dom]},
+        "roofline": ({"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,
+                      "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
+                      "avg_us": stage_avg_us[dom], "flops_per_launch": fl[dom]}
+                     if mfma_bound else
+                     {"bound": "hbm", "kernel": dom, "achieved": dom_gbs, "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "frac": dom_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                      "avg_us": stage_avg_us[dom], "bytes_per_launch": sb[dom]}),
         "layer": {"tflops": layer_tflops, "mfma_frac": layer_tflops / peak,
                   "hbm_gbs_compulsory": w.hbm_bytes() / (ms_per_step * 1e-3) / 1e9,
                   "stage_avg_us": stage_avg_us},

@@ -62,6 +62,28 @@ class Workload:
         st["total"] = sum(st.values())
         return st
 
+    def stage_bytes(self, T: Optional[int] = None) -> dict:
+        """Compulsory bytes per kernel stage: its inputs read once, its outputs
+        written once (weights in the packed form the kernels read: the compute
+        dtype, plus fp32 gain / U_expert / bias / scales)."""
+        T = self.T if T is None else T
+        es = 4 if self.dtype == torch.float32 else 2
+        E_pad = max(32, 1 << (self.E - 1).bit_length())
+        small = 4 * (self.r3 + self.E * self.r1)
+        st = {
+            "front": T * self.d_in * es + (self.r3 + E_pad) * self.d_in * es + small
+                     + T * self.r3 * es + T * self.r1 * 4 + T * self.k * 8,
+            "core": T * self.r3 * es + T * self.r1 * 4 + self.r1 * self.r3 * self.r2 * es
+                    + T * self.r2 * es,
+            "out_proj": T * self.r2 * es + self.d_out * self.r2 * es + 4 * self.d_out
+                        + T * self.d_out * es,
+        }
+        if self.fp8:
+            st["front"] += 4 * self.r3
+            st["core"] += 8 * self.r1 * self.r2
+            st["out_proj"] += 4 * self.d_out
+        return st
+
     def hbm_bytes(self, T: Optional[int] = None) -> int:
         """Compulsory HBM bytes per forward: x in, out, every weight once (fp8
         workloads: the three projections at one byte plus their fp32 scales)."""
