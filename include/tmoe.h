@@ -50,11 +50,22 @@ extern "C" {
  * for TMOE_BF16, applying the scales in fp32. */
 #define TMOE_BF16_FP8W 2
 
+/* router modes (tmoe_shape.router_mode) */
+#define TMOE_ROUTER_SOFTMAX_TOPK 0  /* the reference module: softmax over the k selected logits */
+#define TMOE_ROUTER_CAPPED       1  /* the trained checkpoints' router, see tmoe_shape */
+
 /* Layer hyper-parameters.
  * Replaces TuckerMoE.__init__(d_in, d_out, cfg) (model.py:54-66):
  *   E = cfg.kmoe_num_experts, k = cfg.kmoe_top_k, r1/r2/r3 = cfg.kmoe_r1/_r2/_r3,
  *   eps = cfg.rms_norm_eps (config.py:18,20-24). dtype = the module's parameter
- *   dtype, which the reference forward also computes in. */
+ *   dtype, which the reference forward also computes in.
+ * router_mode TMOE_ROUTER_SOFTMAX_TOPK (0) is model.py:75-77. TMOE_ROUTER_CAPPED (1)
+ * is the router the trained checkpoints use (mamba3_mlx/mlx_model/tucker_moe.py:107-114,
+ * ops.py:9-14): score = router_scale * tanh(logit / router_scale) / router_temperature
+ * with tanh(u) = 2 sigmoid(2u) - 1; top-k by score; weights = softmax over all E of the
+ * scores, taken at the selected experts and divided by (their sum + 1e-6). The
+ * reference's inference values are router_scale = 10, router_temperature = 0.5; both
+ * must be > 0 (unused in mode 0). */
 typedef struct tmoe_shape {
   int64_t d_in, d_out;
   int64_t E, k;
@@ -62,6 +73,8 @@ typedef struct tmoe_shape {
   int32_t dtype;   /* TMOE_BF16 or TMOE_F32: activations, weights and output;
                       TMOE_BF16_FP8W: bf16 activations, e4m3 projection weights */
   float   eps;
+  int32_t router_mode;
+  float   router_scale, router_temperature;
 } tmoe_shape;
 
 typedef struct tmoe_plan tmoe_plan;
@@ -120,9 +133,11 @@ int tmoe_pack_weights_fp8(const tmoe_plan* plan, const void* router_w,
 /* The layer forward for T tokens: out = TuckerMoE.forward(x) (model.py:68-102).
  *   x        (T, d_in)   plan dtype
  *   out      (T, d_out)  plan dtype
- *   topk_idx (T, k) int32, nullable: selected experts, descending logit,
- *            ties to the lower index (torch.topk's indices, model.py:76)
- *   topk_w   (T, k) f32, nullable: softmax over the k selected logits (model.py:77)
+ *   topk_idx (T, k) int32, nullable: selected experts, descending logit (router
+ *            mode 1: descending score), ties to the lower index (torch.topk's
+ *            indices, model.py:76)
+ *   topk_w   (T, k) f32, nullable: the routing weights (mode 0: softmax over the k
+ *            selected logits, model.py:77)
  *   logits   (T, E) f32, nullable: router scores x @ router_w^T (model.py:75)
  *   workspace of at least tmoe_workspace_bytes(plan, T) bytes.
  * T == 0 is a no-op. Stream-ordered, no allocation, no host synchronisation. */

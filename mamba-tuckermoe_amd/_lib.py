@@ -22,6 +22,7 @@ LIB_PATH = os.path.join(HERE, "libtmoe.so")
 ABI_VERSION = 2
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
+TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
 
@@ -41,6 +42,8 @@ class TmoeShape(ctypes.Structure):
         ("E", ctypes.c_int64), ("k", ctypes.c_int64),
         ("r1", ctypes.c_int64), ("r2", ctypes.c_int64), ("r3", ctypes.c_int64),
         ("dtype", ctypes.c_int32), ("eps", ctypes.c_float),
+        ("router_mode", ctypes.c_int32), ("router_scale", ctypes.c_float),
+        ("router_temperature", ctypes.c_float),
     ]
 
 
@@ -112,7 +115,7 @@ class Plan:
     """Owns a tmoe_plan*. Immutable; safe to share across streams."""
 
     def __init__(self, d_in, d_out, E, k, r1, r2, r3, dtype: torch.dtype, eps: float,
-                 fp8_weights: bool = False):
+                 fp8_weights: bool = False, router=(TMOE_ROUTER_SOFTMAX_TOPK, 10.0, 0.5)):
         if fp8_weights:
             if dtype != torch.bfloat16:
                 raise TmoeError(TMOE_EUNSUPPORTED,
@@ -125,7 +128,9 @@ class Plan:
         else:
             raise TmoeError(TMOE_EUNSUPPORTED,
                             f"parameter dtype {dtype}: supported are bfloat16 and float32")
-        self.shape = TmoeShape(d_in, d_out, E, k, r1, r2, r3, code, eps)
+        self.shape = TmoeShape(d_in, d_out, E, k, r1, r2, r3, code, eps, int(router[0]),
+                               float(router[1]), float(router[2]))
+        self.router = tuple(router)
         self.dtype = dtype
         self.fp8_weights = fp8_weights
         self._ptr = ctypes.c_void_p()

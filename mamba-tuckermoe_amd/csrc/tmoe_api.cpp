@@ -5,6 +5,7 @@
 // error path is reachable without a GPU.
 #include <hip/hip_runtime.h>
 
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -113,6 +114,13 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     return fail(TMOE_EINVAL, "top_k=%lld exceeds the number of experts E=%lld", (long long)s.k,
                 (long long)s.E);
   if (!(s.eps >= 0.f)) return fail(TMOE_EINVAL, "eps must be >= 0");
+  if (s.router_mode != TMOE_ROUTER_SOFTMAX_TOPK && s.router_mode != TMOE_ROUTER_CAPPED)
+    return fail(TMOE_EINVAL, "router_mode %d is neither TMOE_ROUTER_SOFTMAX_TOPK nor "
+                             "TMOE_ROUTER_CAPPED", s.router_mode);
+  if (s.router_mode == TMOE_ROUTER_CAPPED &&
+      !(s.router_scale > 0.f && s.router_temperature > 0.f && s.router_scale < INFINITY &&
+        s.router_temperature < INFINITY))
+    return fail(TMOE_EINVAL, "router_scale and router_temperature must be finite and > 0");
   if (s.d_in % 64)
     return fail(TMOE_EUNSUPPORTED, "d_in=%lld: must be a multiple of 64", (long long)s.d_in);
   if (s.r3 != 64 && s.r3 != 128 && s.r3 != 256)
@@ -294,6 +302,9 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
 
   tmoe::FwdArgs a{};
   a.dtype = p->kdtype;
+  a.router_mode = s.router_mode;
+  a.router_scale = s.router_scale;
+  a.router_temperature = s.router_temperature;
   a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
   a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
   a.x = x;

@@ -20,6 +20,8 @@ constexpr int kMaxExperts = 256;
 // Device pointers of one forward, resolved by the host.
 struct FwdArgs {
   int dtype;                    // TMOE_BF16 / TMOE_F32
+  int router_mode;              // TMOE_ROUTER_SOFTMAX_TOPK / TMOE_ROUTER_CAPPED
+  float router_scale, router_temperature;   // router_mode 1
   int64_t T, d_in, d_out, E, E_pad, k, r1, r2, r3;
   float eps;
   const void* x;

@@ -629,6 +629,38 @@ __device__ __forceinline__ void group_max_key(uint64_t& key) {
   if constexpr (G >= 4) dpp_max_step<0x4e>(key);    // quad_perm [2,3,0,1]
   if constexpr (G >= 8) dpp_max_step<0x141>(key);   // row_half_mirror
 }
+// Sum over the same lane groups (every lane ends with the group's sum).
+template <int CTRL>
+__device__ __forceinline__ void dpp_add_step(float& v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int G>
+__device__ __forceinline__ void group_sum(float& v) {
+  if constexpr (G >= 2) dpp_add_step<0xb1>(v);
+  if constexpr (G >= 4) dpp_add_step<0x4e>(v);
+  if constexpr (G >= 8) dpp_add_step<0x141>(v);
+}
+
+// Router score of the trained-checkpoint mode (router_mode 1): the logit capped
+// as scale * tanh(x / scale), tanh(u) taken as 2 sigmoid(2u) - 1, then divided
+// by the temperature (mamba3_mlx/mlx_model/ops.py:9-14,
+// mamba3_mlx/mlx_model/tucker_moe.py:107-109).
+__device__ __forceinline__ float capped_score(float raw, float scale, float temperature) {
+  const float u = raw * (1.f / scale);
+  const float sg = 1.f / (1.f + expf(-2.f * u));
+  return ((2.f * sg - 1.f) * scale) / temperature;
+}
+// Weight of selected slot kk. router_mode 0 (model.py:77): softmax over the k
+// selected logits, ex_kk / sum_j ex_j. router_mode 1 (tucker_moe.py:110-114):
+// softmax over all E, p_kk = ex_kk / sum_all, renormalised over the selected as
+// p_kk / (sum_j p_j + 1e-6). ex = exp(score - max score) throughout.
+__device__ __forceinline__ float slot_weight(int mode, const float* ex, int K, int kk,
+                                             float sum_top, float sum_all) {
+  if (mode == 0) return ex[kk] / sum_top;
+  float ps = 0.f;
+  for (int j = 0; j < K; ++j) ps += ex[j] / sum_all;
+  return (ex[kk] / sum_all) / (ps + 1e-6f);
+}
 
 template <class Elt, int FM, int NR, int NW>
 struct RouterExtra {
@@ -677,9 +709,10 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   constexpr int LD = EP + 1;
   constexpr int kPlanes = RX::kSplitK ? NW : 1;
   constexpr int kZBytes = TileStage<TL, T>::kBytes;
-  // + per-row top-k record: exp weights and indices of the k rounds, and their sum
+  // + per-row top-k record: exp weights, indices and final weights of the k
+  // rounds, the sum over the selected and the sum over all E
   constexpr int kEpiBytes =
-      kZBytes + (kPlanes * BM * LD + NW * BM + BM + BM * (2 * kMaxTopK + 1)) * 4;
+      kZBytes + (kPlanes * BM * LD + NW * BM + BM + BM * (3 * kMaxTopK + 2)) * 4;
   // U_expert is staged after that: at least 4 KB (E = 256, r1 = 4) of room
   constexpr int kSmemBytes = cmax(TL::kLdsBytes, kEpiBytes + 4096);
   __shared__ u32x4 smem[kSmemBytes / 16];
@@ -797,8 +830,11 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
   float* rec_ex = inv + BM;                       // [BM][kMaxTopK]
   int* rec_i = reinterpret_cast<int*>(rec_ex + BM * kMaxTopK);   // [BM][kMaxTopK]
-  float* rec_sum = reinterpret_cast<float*>(rec_i + BM * kMaxTopK);   // [BM]
-  float* ue = rec_sum + BM;
+  float* rec_w = reinterpret_cast<float*>(rec_i + BM * kMaxTopK);   // [BM][kMaxTopK]
+  float* rec_sum = rec_w + BM * kMaxTopK;         // [BM] over the selected
+  float* rec_all = rec_sum + BM;                  // [BM] over all E (router_mode 1)
+  float* ue = rec_all + BM;
+  const int mode = a.router_mode;
   const bool ue_lds = E * R1 * 4 <= kUeBytes;
   if (ue_lds)
     for (int i = threadIdx.x; i < E * R1; i += TL::kThreads) ue[i] = a.uexp[i];
@@ -811,6 +847,7 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
     const bool live = inb && row < rows_valid;
     const int64_t g = m0 + row;
     uint64_t key[PL];   // 0 for columns past E and for taken candidates
+    float sv[PL];       // the scores the keys rank (router_mode 1: capped ones)
 #pragma unroll
     for (int p = 0; p < PL; ++p) {
       const int col = gl + G * p;
@@ -821,8 +858,9 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
       } else {
         sc = lg[row * LD + col];
       }
-      key[p] = col < E ? rank_key(sc, col) : 0;
       if (a.logits && live && col < E) a.logits[g * E + col] = sc;
+      sv[p] = mode ? capped_score(sc, a.router_scale, a.router_temperature) : sc;
+      key[p] = col < E ? rank_key(sv[p], col) : 0;
     }
     float vmax = 0.f, ssum = 0.f;
 #pragma unroll 1
@@ -844,21 +882,31 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
         rec_i[row * kMaxTopK + kk] = bi;
       }
     }
+    if (mode) {   // softmax denominator over all E
+      float sa = 0.f;
+#pragma unroll
+      for (int p = 0; p < PL; ++p) sa += gl + G * p < E ? expf(sv[p] - vmax) : 0.f;
+      group_sum<G>(sa);
+      if (gl == 0 && inb) rec_all[row] = sa;
+    }
     if (gl == 0 && inb) rec_sum[row] = ssum;
   }
   __syncthreads();
-  // softmax weights (model.py:77) and c = sum_j w_j U_expert[e_j] (model.py:93)
+  // routing weights (model.py:77) and c = sum_j w_j U_expert[e_j] (model.py:93)
   for (int q = threadIdx.x; q < rows_valid * K; q += TL::kThreads) {
     const int row = q / K, kk = q - row * K;
+    const float wk = slot_weight(mode, rec_ex + row * kMaxTopK, K, kk, rec_sum[row],
+                                 mode ? rec_all[row] : 0.f);
     a.idx[(m0 + row) * K + kk] = rec_i[row * kMaxTopK + kk];
-    a.w[(m0 + row) * K + kk] = rec_ex[row * kMaxTopK + kk] / rec_sum[row];
+    a.w[(m0 + row) * K + kk] = wk;
+    rec_w[row * kMaxTopK + kk] = wk;
   }
+  __syncthreads();
   for (int q = threadIdx.x; q < rows_valid * R1; q += TL::kThreads) {
     const int row = q / R1, r = q - row * R1;
-    const float sum = rec_sum[row];
     float cr = 0.f;
     for (int kk = 0; kk < K; ++kk)
-      cr += (rec_ex[row * kMaxTopK + kk] / sum) * uex[rec_i[row * kMaxTopK + kk] * R1 + r];
+      cr += rec_w[row * kMaxTopK + kk] * uex[rec_i[row * kMaxTopK + kk] * R1 + r];
     a.c[(m0 + row) * R1 + r] = cr;
   }
 }

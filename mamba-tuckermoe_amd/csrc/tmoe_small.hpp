@@ -234,15 +234,18 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) 
       store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, (zv[q] * inv_rms) * a.gain[j]);
   }
   uint64_t key[4];   // rank_key order; 0 past E and once taken
+  float sv[4];       // the ranked scores (router_mode 1: capped ones)
+  const int mode = a.router_mode;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = lane + 64 * q;
     const float lv = e < E ? row[R3 + e] : 0.f;
-    key[q] = e < E ? rank_key(lv, e) : 0;
     if (a.logits && e < E) a.logits[t * E + e] = lv;
+    sv[q] = mode ? capped_score(lv, a.router_scale, a.router_temperature) : lv;
+    key[q] = e < E ? rank_key(sv[q], e) : 0;
   }
   // K rounds of a wave max-key; lane kk keeps round kk's winner (K <= 16 < 64)
-  float sv = 0.f;
+  float selv = 0.f;
   int si = 0;
 #pragma unroll 1
   for (int kk = 0; kk < K; ++kk) {
@@ -259,16 +262,29 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) 
 #pragma unroll
     for (int q = 0; q < 4; ++q) key[q] = key[q] == best ? 0 : key[q];
     if (kk == lane) {   // k <= E: best names a candidate, index < E
-      sv = key_value(best);
+      selv = key_value(best);
       si = key_index(best);
     }
   }
-  const float vmax = __shfl(sv, 0);
-  const float ex = lane < K ? expf(sv - vmax) : 0.f;
+  const float vmax = __shfl(selv, 0);
+  const float ex = lane < K ? expf(selv - vmax) : 0.f;
   float ssum = ex;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) ssum += __shfl_xor(ssum, off);
-  const float wk = ex / ssum;
+  float wk;
+  if (mode) {
+    // softmax over all E, then the selected renormalised (+1e-6)
+    float sa = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sa += lane + 64 * q < E ? expf(sv[q] - vmax) : 0.f;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sa += __shfl_xor(sa, off);
+    float ps = 0.f;
+    for (int j = 0; j < K; ++j) ps += __shfl(ex, j) / sa;
+    wk = (ex / sa) / (ps + 1e-6f);
+  } else {
+    wk = ex / ssum;
+  }
   if (lane < K) {
     a.idx[t * K + lane] = si;
     a.w[t * K + lane] = wk;

@@ -67,6 +67,7 @@ class TuckerMoE(nn.Module):
         self._packed_key = None
         self._warned_grad = False
         self._fp8: Optional[dict] = None   # e4m3 codes (uint8) and fp32 scales
+        self._router = (_lib.TMOE_ROUTER_SOFTMAX_TOPK, 10.0, 0.5)
 
     # -- packed-weight cache -------------------------------------------------
     def _params(self):
@@ -85,13 +86,40 @@ class TuckerMoE(nn.Module):
     def plan(self) -> _lib.Plan:
         dtype = self.U_in.dtype
         fp8 = self._fp8 is not None
-        if self._plan is None or self._plan.dtype != dtype or self._plan.fp8_weights != fp8:
+        if (self._plan is None or self._plan.dtype != dtype or self._plan.fp8_weights != fp8
+                or self._plan.router != self._router):
             d_in, r3 = self.U_in.shape
             r2, d_out = self.U_out.shape
             E, r1 = self.U_expert.shape
             self._plan = _lib.Plan(d_in, d_out, E, self.top_k, r1, r2, r3, dtype,
-                                   float(self.inner_norm.eps), fp8_weights=fp8)
+                                   float(self.inner_norm.eps), fp8_weights=fp8,
+                                   router=self._router)
         return self._plan
+
+    # -- router mode -------------------------------------------------------------
+    def set_router_mode(self, mode: str = "softmax_topk", scale: float = 10.0,
+                        temperature: float = 0.5) -> None:
+        """"softmax_topk" (default): the reference module's router, model.py:75-77.
+        "capped": the router the trained checkpoints use
+        (mamba3_mlx/mlx_model/tucker_moe.py:107-114): scores = scale *
+        tanh(logits / scale) / temperature, top-k of the scores, weights = the
+        softmax over all experts at the selected ones / (their sum + 1e-6)."""
+        if mode == "softmax_topk":
+            self._router = (_lib.TMOE_ROUTER_SOFTMAX_TOPK, 10.0, 0.5)
+        elif mode == "capped":
+            if not (scale > 0 and temperature > 0):
+                raise ValueError("scale and temperature must be > 0")
+            self._router = (_lib.TMOE_ROUTER_CAPPED, float(scale), float(temperature))
+        else:
+            raise ValueError(f"router mode {mode!r}: 'softmax_topk' or 'capped'")
+        self._plan = None
+
+    @property
+    def router_mode(self):
+        """("softmax_topk",) or ("capped", scale, temperature)."""
+        if self._router[0] == _lib.TMOE_ROUTER_CAPPED:
+            return ("capped", self._router[1], self._router[2])
+        return ("softmax_topk",)
 
     # -- fp8 weights -----------------------------------------------------------
     def load_fp8(self, U_in_q, U_in_scale, core_q, core_scale, U_out_q, U_out_scale) -> None:

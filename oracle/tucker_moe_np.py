@@ -13,6 +13,12 @@ restatement (tucker_moe_torch.py) and, at full sizes, the GPU results:
 
 brute_force() restates the same layer with pure-Python loops, in the
 reference's own grouping (per slot, G_j = sum_r g_jr core[r]), for tiny shapes.
+
+router=("capped", scale, temperature) states the trained checkpoints' router
+(mamba3_mlx/mlx_model/tucker_moe.py:107-114) from its definition: scores =
+scale * tanh(logits / scale) / temperature (tanh itself, which the reference's
+2 sigmoid(2u) - 1 equals), top-k of the scores, P = softmax(scores) over all E,
+w = P[top-k] / (sum P[top-k] + 1e-6).
 """
 from __future__ import annotations
 
@@ -23,12 +29,14 @@ import numpy as np
 
 
 def _np(p):
-    return {k: np.asarray(v.detach().cpu().float().numpy() if hasattr(v, "detach") else v,
+    return {k: np.asarray(v.detach().cpu().double().numpy() if hasattr(v, "detach") else v,
                           dtype=np.float64) for k, v in p.items()}
 
 
-def forward_f64(x, params: Dict, top_k: int, eps: float = 1e-5, chunk: int = 4096) -> Dict:
-    """Returns dict(logits, idx (int64), w, z, c, mid, out) in float64.
+def forward_f64(x, params: Dict, top_k: int, eps: float = 1e-5, chunk: int = 4096,
+                router=None) -> Dict:
+    """Returns dict(logits, scores, idx (int64), w, z, c, mid, out) in float64
+    (scores: what top-k ranks; the logits unless router is "capped").
 
     x: (T, d_in) array or tensor; params: state_dict-keyed arrays or tensors."""
     p = _np(params)
@@ -38,14 +46,22 @@ def forward_f64(x, params: Dict, top_k: int, eps: float = 1e-5, chunk: int = 409
     U_exp, core, U_out, bias = p["U_expert"], p["core"], p["U_out"], p["bias"]
     r1, r3, r2 = core.shape
     P = core.transpose(1, 0, 2).reshape(r3, r1 * r2)     # z @ P = [z @ core[r]]_r
-    res = {k: [] for k in ("logits", "idx", "w", "z", "c", "mid", "out")}
+    res = {k: [] for k in ("logits", "scores", "idx", "w", "z", "c", "mid", "out")}
+    capped = router is not None and router[0] == "capped"
     for s in range(0, X.shape[0], chunk):
         Xc = X[s:s + chunk]
         S = Xc @ Wr.T
-        idx = np.argsort(-S, axis=1, kind="stable")[:, :top_k]
-        v = np.take_along_axis(S, idx, axis=1)
-        e = np.exp(v - v[:, :1])
-        w = e / e.sum(axis=1, keepdims=True)
+        L = router[1] * np.tanh(S / router[1]) / router[2] if capped else S
+        idx = np.argsort(-L, axis=1, kind="stable")[:, :top_k]
+        if capped:
+            prob = np.exp(L - L.max(axis=1, keepdims=True))
+            prob /= prob.sum(axis=1, keepdims=True)
+            top = np.take_along_axis(prob, idx, axis=1)
+            w = top / (top.sum(axis=1, keepdims=True) + 1e-6)
+        else:
+            v = np.take_along_axis(S, idx, axis=1)
+            e = np.exp(v - v[:, :1])
+            w = e / e.sum(axis=1, keepdims=True)
         zr = Xc @ U_in
         rms = np.sqrt(np.mean(zr * zr, axis=1, keepdims=True) + eps)
         z = zr / rms * g
@@ -53,8 +69,8 @@ def forward_f64(x, params: Dict, top_k: int, eps: float = 1e-5, chunk: int = 409
         Y = (z @ P).reshape(-1, r1, r2)
         mid = np.einsum("tr,trj->tj", c, Y)
         out = mid @ U_out + bias
-        for k_, v_ in (("logits", S), ("idx", idx), ("w", w), ("z", z), ("c", c), ("mid", mid),
-                       ("out", out)):
+        for k_, v_ in (("logits", S), ("scores", L), ("idx", idx), ("w", w), ("z", z), ("c", c),
+                       ("mid", mid), ("out", out)):
             res[k_].append(v_)
     return {k: (np.concatenate(v) if v else None) for k, v in res.items()}
 

@@ -36,6 +36,28 @@ def route(xf: torch.Tensor, router_w: torch.Tensor, top_k: int):
     return scores, topk_idx, F.softmax(topk_v, dim=-1)
 
 
+def tanh_approx(x: torch.Tensor) -> torch.Tensor:
+    """mamba3_mlx/mlx_model/ops.py:9-10: 2 sigmoid(2x) - 1."""
+    return 2.0 * torch.sigmoid(2.0 * x) - 1.0
+
+
+def route_capped(xf: torch.Tensor, router_w: torch.Tensor, top_k: int, scale: float,
+                 temperature: float):
+    """The trained checkpoints' router, mamba3_mlx/mlx_model/tucker_moe.py:107-114 (with
+    ops.py:13-14 scaled_tanh): raw logits in fp32, capped = tanh_approx(raw / scale) *
+    scale, scores = capped / temperature, probs = softmax over all E, top-k of the
+    scores (torch.topk order: descending, as sft_cot_bundle/scripts/model.py:327),
+    weights = probs at the selected experts / (their sum + 1e-6). Returns the raw
+    logits, the indices and the weights."""
+    raw = F.linear(xf, router_w)
+    capped = tanh_approx(raw.float() * (1.0 / scale)) * scale
+    scores = capped / temperature
+    probs = torch.softmax(scores, dim=-1)
+    _, topk_idx = torch.topk(scores, top_k, dim=-1)
+    top = probs.gather(-1, topk_idx)
+    return raw, topk_idx, (top / (top.sum(-1, keepdim=True) + 1e-6)).to(raw.dtype)
+
+
 def project_in(xf, U_in, inner_w, eps):
     """model.py:80-81."""
     return rmsnorm(xf @ U_in, inner_w, eps)
@@ -62,7 +84,7 @@ STAGES = {"route": route, "project_in": project_in, "core_contract": core_contra
 
 def forward(x: torch.Tensor, params: Dict[str, torch.Tensor], top_k: int, eps: float = 1e-5,
             chunk: int = 512, compute_dtype: Optional[torch.dtype] = None,
-            intermediates: bool = False, stages: Optional[dict] = None):
+            intermediates: bool = False, stages: Optional[dict] = None, router=None):
     """TuckerMoE.forward (model.py:68-102) on the CPU.
 
     x: (..., d_in). params: state_dict-keyed tensors. Returns out (..., d_out) in
@@ -70,7 +92,8 @@ def forward(x: torch.Tensor, params: Dict[str, torch.Tensor], top_k: int, eps: f
     a dict with logits (T, E), idx (T, k) int64, w (T, k), z (T, r3),
     mid (T, r2) and out.
     `stages` replaces stage functions by name (used by the tests' planted
-    mistakes)."""
+    mistakes). `router` = ("capped", scale, temperature) selects route_capped
+    instead of the reference module's route."""
     st = dict(STAGES)
     if stages:
         st.update(stages)
@@ -84,7 +107,10 @@ def forward(x: torch.Tensor, params: Dict[str, torch.Tensor], top_k: int, eps: f
         xf = xf_all[s:s + chunk]
         if xf.shape[0] == 0:
             break
-        logits, idx, w = st["route"](xf, p["router.weight"], top_k)
+        if router is not None and router[0] == "capped":
+            logits, idx, w = route_capped(xf, p["router.weight"], top_k, router[1], router[2])
+        else:
+            logits, idx, w = st["route"](xf, p["router.weight"], top_k)
         z = st["project_in"](xf, p["U_in"], p["inner_norm.weight"], eps)
         mid = st["core_contract"](z, idx, w, p["U_expert"], p["core"])
         out = st["project_out"](mid, p["U_out"], p["bias"])

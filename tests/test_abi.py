@@ -55,6 +55,9 @@ def _create(pkg, **kw):
     (dict(E=300, k=2), -2, "E=300"),
     (dict(E=32, k=17), -2, "top_k=17"),
     (dict(r1=65), -2, "r1"),
+    (dict(router_mode=2), -1, "router_mode"),
+    (dict(router_mode=1, router_scale=0.0, router_temperature=0.5), -1, "router_scale"),
+    (dict(router_mode=1, router_scale=10.0, router_temperature=-1.0), -1, "router_temperature"),
 ])
 def test_plan_create_rejects(pkg, kw, code, msg):
     rc, p, err = _create(pkg, **kw)

@@ -281,3 +281,94 @@ def test_e4m3_dequantize_layouts():
     s2 = g.random(6)
     w2 = e4m3.dequantize(q2, s2, "U_out")
     assert np.array_equal(w2, e4m3.decode(q2) * s2[None, :])
+
+
+# ---- the trained checkpoints' router ("capped") --------------------
+
+def _capped_case(E=12, k=3, T=40, seed=7):
+    w = pkg_workload(E, k, T, seed)
+    return w
+
+
+def pkg_workload(E, k, T, seed):
+    import importlib.util, os, sys
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    return pkg, pkg.Workload("capped", T, 64, 48, E, k, 2, 64, 64, torch.float32, seed)
+
+
+def test_tanh_approx_is_tanh():
+    u = torch.linspace(-30, 30, 2001, dtype=torch.float64)
+    assert torch.allclose(ot.tanh_approx(u), torch.tanh(u), rtol=0, atol=1e-15)
+
+
+@pytest.mark.parametrize("scale,temp,mult", [(10.0, 0.5, 40), (3.0, 2.0, 8)])
+def test_capped_router_torch_matches_f64(scale, temp, mult):
+    pkg, w = _capped_case()
+    params = pkg.synth.make_params(w, affine="random")
+    # larger router weights so that the cap and the temperature matter
+    params["router.weight"] = params["router.weight"] * mult
+    x = pkg.synth.make_x(w)
+    r = ("capped", scale, temp)
+    t = ot.forward(x, params, w.k, compute_dtype=torch.float32, intermediates=True, router=r)
+    f = onp.forward_f64(x, params, w.k, router=r)
+    # where the cap saturates, fp32 tanh returns exactly 1 and ties scores that
+    # float64 still separates: compare routing on rows with a resolvable gap
+    gap = onp.topk_gap(f["scores"], w.k)
+    ok = gap > 1e-4
+    assert ok.mean() > 0.5
+    assert np.array_equal(t["idx"].numpy()[ok], f["idx"][ok])
+    # fp32 scores near 20 carry ~2e-6 absolute rounding, which the exp passes on
+    assert np.abs(t["w"].double().numpy()[ok] - f["w"][ok]).max() < 5e-6
+    assert onp.rel_l2(t["out"].double().numpy()[ok], f["out"][ok]) < 1e-5
+    # the cap is active: some scores are well inside the saturation region
+    assert np.abs(f["logits"]).max() > scale
+
+
+def test_capped_router_all_experts_closed_form():
+    pkg, w = _capped_case(E=5, k=5)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    f = onp.forward_f64(x, params, w.k, router=("capped", 10.0, 0.5))
+    L = 10.0 * np.tanh(f["logits"] / 10.0) / 0.5
+    P = np.exp(L - L.max(1, keepdims=True))
+    P /= P.sum(1, keepdims=True)
+    # k = E: every expert is selected, so w = P (in score order) / (1 + 1e-6)
+    assert np.allclose(f["w"], np.take_along_axis(P, f["idx"], 1) / (1 + 1e-6), rtol=1e-12)
+    assert np.allclose(f["w"].sum(1), 1 / (1 + 1e-6), rtol=1e-12)
+
+
+def test_capped_router_same_indices_below_saturation():
+    pkg, w = _capped_case()
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    a = onp.forward_f64(x, params, w.k)
+    b = onp.forward_f64(x, params, w.k, router=("capped", 10.0, 0.5))
+    assert np.abs(a["logits"]).max() < 5.0        # far from the cap: tanh is strictly monotone
+    assert np.array_equal(a["idx"], b["idx"])
+    assert not np.allclose(a["w"], b["w"], atol=1e-3)   # but the temperature changes the weights
+
+
+@pytest.mark.parametrize("mistake", ["no_temperature", "no_eps", "uncapped"])
+def test_capped_router_planted_mistakes(mistake):
+    """A wrong restatement of the capped router fails the float64 formulation."""
+    pkg, w = _capped_case(E=6, k=6)
+    params = pkg.synth.make_params(w, affine="random")
+    params["router.weight"] = params["router.weight"] * 40
+    x = pkg.synth.make_x(w)
+    scale, temp = 10.0, 0.5
+
+    def bad(xf, router_w, top_k):
+        raw = torch.nn.functional.linear(xf, router_w)
+        capped = raw if mistake == "uncapped" else ot.tanh_approx(raw / scale) * scale
+        sc = capped if mistake == "no_temperature" else capped / temp
+        probs = torch.softmax(sc, -1)
+        _, idx = torch.topk(sc, top_k, -1)
+        top = probs.gather(-1, idx)
+        den = top.sum(-1, keepdim=True) + (0.0 if mistake == "no_eps" else 1e-6)
+        return raw, idx, top / den
+
+    t = ot.forward(x, params, w.k, compute_dtype=torch.float64, intermediates=True,
+                   stages={"route": bad})
+    f = onp.forward_f64(x, params, w.k, router=("capped", scale, temp))
+    assert np.abs(t["w"].numpy() - f["w"]).max() > 1e-7
