@@ -12,7 +12,7 @@ namespace tmoe {
 // 32 f32 elements.
 constexpr int kTileKBytes = 128;
 constexpr int kFrontBM = 64;    // tokens per k_front work-group (whole r3 and E rows)
-constexpr int kFrontPFA = 2;    // K tiles of x in flight per k_front work-group
+constexpr int kFrontPFA = 8;    // K tiles of x in flight per k_front work-group
 constexpr int kFrontWM = 2;     // row groups of waves per k_front work-group
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 256;

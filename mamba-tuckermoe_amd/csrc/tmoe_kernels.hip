@@ -22,12 +22,16 @@ struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 
 
 // Front tiles: kFrontBM tokens in kFrontWM row groups; with the widest router
 // (E > 128) one group of 32 tokens, whose smaller LDS footprint measured faster.
+// The weight rows come from L2 one DMA per K tile; a third LDS stage (when it
+// fits) issues them two tiles ahead, which hides the L2 latency.
 template <class Elt, int R3, int NR>
 hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
   constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
+  constexpr int kStageBytes = (BM + R3 + 32 * NR) * 128;
+  constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
   const dim3 grid(cdiv(a.T, BM)), block(64 * NW * WM);
-  hipLaunchKernelGGL((dev::k_front<Elt, R3, NR, kFrontPFA, BM, 2, WM>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((dev::k_front<Elt, R3, NR, kFrontPFA, BM, NS, WM>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 

@@ -45,8 +45,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);   // round to nearest even
 }
+// Two floats to two bf16 (round to nearest even) in one register; as a vector
+// conversion this is a single v_cvt_pk_bf16_f32.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ float load_as_f32(const uint16_t* p) { return bf16_bits_to_f32(*p); }
@@ -162,28 +167,30 @@ struct KhatriRaoLoader {
 //  * a register ring of PFA / PFB tiles (for an operand that is transformed on
 //    the way, or streamed from HBM and wanting more tiles in flight); tile kt+1
 //    is written to LDS in between the MFMAs of tile kt.
+// WA > 0 splits the loads by wave: waves 0 .. WA-1 run the register rings and
+// issue no DMA, the others issue the DMA and no register loads (see
+// gemm_mainloop).
 // One barrier per K tile, preceded by an explicit wait for exactly the loads
 // tile kt + 1 needs (the compiler's own barrier would wait for every load).
 template <int BM_, int BN_, int BX_, int WM_, int WN_, int PFA_, int PFB_, int NS_ = 2,
-          bool ADMA_ = false, bool BDMA_ = false>
+          bool ADMA_ = false, bool BDMA_ = false, int WA_ = 0>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, BX = BX_, WM = WM_, WN = WN_;
-  static constexpr int PFA = PFA_, PFB = PFB_, NS = NS_;
+  static constexpr int PFA = PFA_, PFB = PFB_, NS = NS_, WA = WA_;
   static constexpr bool ADMA = ADMA_, BDMA = BDMA_;
   static constexpr int kThreads = 64 * WM * WN;
   static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
   static constexpr int FM = kWaveM / 32, FN = kWaveN / 32;
   static constexpr int kChunks = kTileKBytes / 16;   // 8 per row
   static constexpr int kBRows = BN + BX;
-  // register-staged chunks each thread moves per K tile
-  static constexpr int kAPerThread = (BM * kChunks + kThreads - 1) / kThreads;
-  static constexpr int kBPerThread = (kBRows * kChunks + kThreads - 1) / kThreads;
   static constexpr int kStage = (BM + kBRows) * kChunks;  // u32x4 slots per stage
   static constexpr int kLdsBytes = NS * kStage * 16;
   static_assert(BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile/wave mismatch");
   static_assert(PFA >= 1 && PFA <= 8 && PFB >= 1 && PFA % PFB == 0, "prefetch rings");
   static_assert(NS >= 2 && NS <= 4, "LDS stages");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  static_assert(WA >= 0 && WA < WM * WN, "load roles");
+  static_assert(WA == 0 || (!ADMA && BDMA), "load roles: A by register ring, B by DMA");
 };
 
 typedef __attribute__((address_space(3))) void* lds_vptr;
@@ -219,55 +226,80 @@ __device__ __forceinline__ int dma_chunk(int lane, int blk) {
   return (lane & 7) ^ ((lane >> 4) | ((blk & 1) << 2));
 }
 
-// A main-loop consumer: operator() runs after every K step's MFMAs with that
-// step's A fragments; tile_begin(kt, acc) runs before the MFMAs of K tile kt.
+// A main-loop consumer: load(frag, s, kstep, ch) reads what K step kstep needs
+// from the stage (issued with the main operands' fragments, one step ahead),
+// compute(frag, kstep, af) runs after that step's MFMAs with its A fragments;
+// tile_begin(kt, acc) runs before the MFMAs of K tile kt.
 __device__ __forceinline__ int cmin_dev(int a, int b) { return a < b ? a : b; }
 
 struct NoExtra {
+  struct Frag {};
+  __device__ __forceinline__ void load(Frag&, const u32x4*, int, int) const {}
   template <class AF>
-  __device__ __forceinline__ void operator()(const u32x4*, int, int, const AF&) const {}
+  __device__ __forceinline__ void compute(const Frag&, int, const AF&) const {}
   template <class ACC>
   __device__ __forceinline__ void tile_begin(int, ACC&) const {}
 };
 
-template <class TL, class Elt, class ALoad, class BLoad, class Extra>
-__device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], const ALoad& aload,
-                                              const BLoad& bload, int nkt, u32x4* smem,
-                                              Extra& extra) {
+// One wave's part of the main loop. ROLE 0: every load kind; ROLE 1: the
+// register rings only (waves 0 .. WA-1); ROLE 2: the DMA only (waves WA ..).
+//
+// Every iteration issues the same loads: near the end of K the DMA and the ring
+// refills fetch the last tile again (in bounds; into a stage or ring slot no
+// later tile reads), so the vmcnt bounds below are exact and the compiler's own
+// waits for the ring registers see the same count of younger loads in every
+// iteration (conditional loads made it wait for all of them). Only the tail of
+// nkt % PFA tiles runs under a condition.
+template <int ROLE, class TL, class Elt, class ALoad, class BLoad, class Extra>
+__device__ __forceinline__ void gemm_mainloop_role(f32x16 (&acc)[TL::FM][TL::FN],
+                                                   const ALoad& aload, const BLoad& bload,
+                                                   int nkt, u32x4* smem, Extra& extra) {
   constexpr int FM = TL::FM, FN = TL::FN, CH = TL::kChunks, NS = TL::NS;
   constexpr bool ADMA = TL::ADMA, BDMA = TL::BDMA;
   constexpr int PFA = ADMA ? 1 : TL::PFA, PFB = BDMA ? 1 : TL::PFB;
   constexpr int kKSteps = kTileKBytes / 32;   // MFMA K steps per K tile
   constexpr int W = TL::kThreads / 64;
   constexpr int kARows = TL::BM, kBRows = TL::kBRows;
-  constexpr int AP = ADMA ? 0 : TL::kAPerThread, BP = BDMA ? 0 : TL::kBPerThread;
-  // DMA instructions each wave issues per tile. When the 8-row blocks do not
+  constexpr bool kRing = ROLE != 2, kDma = ROLE != 1;
+  // threads sharing the ring loads, waves sharing the DMA
+  constexpr int NL = ROLE == 1 ? 64 * TL::WA : TL::kThreads;
+  constexpr int NWD = ROLE == 2 ? W - TL::WA : W;
+  constexpr int AP = (kRing && !ADMA) ? (kARows * CH + NL - 1) / NL : 0;
+  constexpr int BP = (kRing && !BDMA) ? (kBRows * CH + NL - 1) / NL : 0;
+  // every ring thread issues the same loads, so one vmcnt count holds for all
+  static_assert(AP * NL == (kRing && !ADMA ? kARows * CH : 0), "register-staged A: full rounds");
+  static_assert(BP * NL == (kRing && !BDMA ? kBRows * CH : 0), "register-staged B: full rounds");
+  // DMA instructions each DMA wave issues per tile. When the 8-row blocks do not
   // split evenly over the waves, the extra slots repeat the last block: the same
   // bytes to the same LDS slots, waited for like any other, so every wave issues
   // the same count and one vmcnt bound holds for all.
   constexpr int kANBlk = kARows / 8, kBNBlk = kBRows / 8;
-  constexpr int ADN = ADMA ? (kANBlk + W - 1) / W : 0, BDN = BDMA ? (kBNBlk + W - 1) / W : 0;
+  constexpr int ADN = (kDma && ADMA) ? (kANBlk + NWD - 1) / NWD : 0;
+  constexpr int BDN = (kDma && BDMA) ? (kBNBlk + NWD - 1) / NWD : 0;
   static_assert(kARows % 16 == 0 && kBRows % 8 == 0, "DMA blocks of 8 rows");
-  // every thread issues the same loads, so one vmcnt count holds for all waves
-  static_assert(ADMA || AP * TL::kThreads == kARows * CH, "register-staged A: full rounds");
-  static_assert(BDMA || BP * TL::kThreads == kBRows * CH, "register-staged B: full rounds");
   // vector memory instructions per tile: register rings (per fetch) and DMA
   constexpr int FA = AP * ALoad::kVmem, FB = BP * BLoad::kVmem, D = ADN + BDN;
-  // loads issued after tile kt+1's DMA until the end of iteration kt (steady state)
+  // loads issued after tile kt+1's DMA until the end of iteration kt
   constexpr int kVmAfter = (NS - 2) * D + (NS - 1) * (FA + FB);
+  static_assert(kVmAfter < 63 && (NS - 2) * D + PFA * FA + PFB * FB < 63, "vmcnt range");
   // Memory instructions are spread over the K steps of a tile, each after that
   // step's MFMAs, so a wave never stalls on a full memory queue with MFMAs left
   // to issue: DMA of tile kt + NS - 1 over the first kDmaSteps steps; the
   // register-staged LDS stores of tile kt + 1 and the ring refills that reuse
-  // their registers over the last kStashSteps steps.
-  constexpr int kStashSteps = 2;
+  // their registers over the last kStashSteps steps (all steps for a wave that
+  // issues no DMA).
+  constexpr int kStashSteps = D > 0 ? 2 : kKSteps;
   constexpr int kDmaSteps = AP + BP > 0 ? kKSteps - kStashSteps : kKSteps;
   constexpr int kPerStep = (AP + BP + kStashSteps - 1) / kStashSteps;
-  constexpr int kDmaPerStep = (ADN + BDN + kDmaSteps - 1) / kDmaSteps;
+  constexpr int kDmaPerStep = (D + (kDmaSteps > 0 ? kDmaSteps : 1) - 1) / (kDmaSteps > 0 ? kDmaSteps : 1);
+  // fragment buffers: two (reads one K step ahead) when the registers allow
+  constexpr int PIPE = FM + FN <= 4 ? 2 : 1;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
+  const int rtid = ROLE == 2 ? tid - 64 * TL::WA : tid;   // index within the role
+  const int rwave = rtid >> 6;
 
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -281,14 +313,14 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
   auto fetch_a = [&](int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < AP; ++i) {
-      const int q = tid + i * TL::kThreads;
+      const int q = rtid + i * NL;
       ra[slot][i] = aload.fetch(q / CH, q % CH, kt);
     }
   };
   auto fetch_b = [&](int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
-      const int q = tid + i * TL::kThreads;
+      const int q = rtid + i * NL;
       rb[slot][i] = bload.fetch(q / CH, q % CH, kt);
     }
   };
@@ -297,17 +329,17 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
   auto dma_one = [&](int j, int kt, int stage) __attribute__((always_inline)) {
     u32x4* s = smem + stage * TL::kStage;
     if (j < ADN) {
-      if constexpr (ADMA) {
-        const int blk = cmin_dev(wave + j * W, kANBlk - 1);
+      if constexpr (ADN > 0) {
+        const int blk = cmin_dev(rwave + j * NWD, kANBlk - 1);
         __builtin_amdgcn_global_load_lds(
             (gbl_cvptr)aload.gaddr(blk * 8 + (lane >> 3), dma_chunk(lane, blk), kt),
             (lds_vptr)(s + blk * 64), 16, 0, 0);
       }
     } else if (j < ADN + BDN) {
-      if constexpr (BDMA) {
+      if constexpr (BDN > 0) {
         // kARows is a multiple of 16, so the block parity within B equals the
         // parity of its LDS block
-        const int blk = cmin_dev(wave + (j - ADN) * W, kBNBlk - 1);
+        const int blk = cmin_dev(rwave + (j - ADN) * NWD, kBNBlk - 1);
         __builtin_amdgcn_global_load_lds(
             (gbl_cvptr)bload.gaddr(blk * 8 + (lane >> 3), dma_chunk(lane, blk), kt),
             (lds_vptr)(s + (kARows + blk * 8) * 8), 16, 0, 0);
@@ -316,67 +348,90 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
   };
   auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < ADN + BDN; ++j) dma_one(j, kt, stage);
+    for (int j = 0; j < D; ++j) dma_one(j, kt, stage);
   };
   // ring refill of register-staged chunk c for tile kt (A slot sa / B slot sb)
-  auto refill_chunk = [&](int c, int kt, int sa, int sb) __attribute__((always_inline)) {
+  auto refill_chunk = [&](int c, int kta, int ktb, int sa, int sb) __attribute__((always_inline)) {
     if (c < AP) {
-      const int q = tid + c * TL::kThreads;
-      ra[sa][c] = aload.fetch(q / CH, q % CH, kt);
+      const int q = rtid + c * NL;
+      ra[sa][c] = aload.fetch(q / CH, q % CH, kta);
     } else if (c < AP + BP) {
-      const int q = tid + (c - AP) * TL::kThreads;
-      rb[sb][c - AP] = bload.fetch(q / CH, q % CH, kt);
+      const int q = rtid + (c - AP) * NL;
+      rb[sb][c - AP] = bload.fetch(q / CH, q % CH, ktb);
     }
   };
   // register-staged chunk c < AP + BP: A chunks first, then B chunks
   auto stash_chunk = [&](int c, int sa, int sb, u32x4* s) __attribute__((always_inline)) {
     if (c < AP) {
-      const int q = tid + c * TL::kThreads;
+      const int q = rtid + c * NL;
       s[lds_slot(q / CH, q % CH)] = aload.finish(ra[sa][c]);
     } else if (c < AP + BP) {
-      const int q = tid + (c - AP) * TL::kThreads;
+      const int q = rtid + (c - AP) * NL;
       s[lds_slot(kARows + q / CH, q % CH)] = bload.finish(rb[sb][c - AP]);
     }
   };
   // MFMAs of tile kt, with the memory work of this iteration in between: DMA of
   // tile kt + NS - 1; stores of ring slots (sa, sb) (tile kt + 1) to that tile's
-  // stage and their refill with tiles kt + 1 + PFA / kt + 1 + PFB.
-  auto compute = [&](int kt, int sa, int sb) __attribute__((always_inline)) {
-    const bool stash = kt + 1 < nkt;
-    const bool do_dma = kt + NS - 1 < nkt;
-    const bool refill_a = kt + 1 + PFA < nkt, refill_b = kt + 1 + PFB < nkt;
+  // stage and their refill with tiles kt + 1 + PFA / kt + 1 + PFB. Past the last
+  // tile these fetch tile nkt - 1 again.
+  auto iteration = [&](int kt, int sa, int sb) __attribute__((always_inline)) {
+    const int ktd = cmin_dev(kt + NS - 1, nkt - 1);
+    const int kta = cmin_dev(kt + 1 + PFA, nkt - 1), ktb = cmin_dev(kt + 1 + PFB, nkt - 1);
     const u32x4* s = smem + (kt % NS) * TL::kStage;
     u32x4* so = smem + ((kt + 1) % NS) * TL::kStage;
-#pragma unroll
-    for (int ks = 0; ks < kKSteps; ++ks) {
+    const int sd = (kt + NS - 1) % NS;
+    extra.tile_begin(kt, acc);
+    // fragments of K step ks in buffer ks % PIPE; with two buffers step ks + 1 is
+    // read before step ks's MFMAs issue
+    u32x4 af[PIPE][FM], bfr[PIPE][FN];
+    typename Extra::Frag xf[PIPE];
+    auto load_frags = [&](int ks, int b) __attribute__((always_inline)) {
       const int ch = ks * 2 + (lane >> 5);
-      u32x4 af[FM], bfr[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = s[lds_slot(wm * TL::kWaveM + i * 32 + (lane & 31), ch)];
+      for (int i = 0; i < FM; ++i)
+        af[b][i] = s[lds_slot(wm * TL::kWaveM + i * 32 + (lane & 31), ch)];
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = s[lds_slot(kARows + wn * TL::kWaveN + j * 32 + (lane & 31), ch)];
+        bfr[b][j] = s[lds_slot(kARows + wn * TL::kWaveN + j * 32 + (lane & 31), ch)];
+      extra.load(xf[b], s, kt * kKSteps + ks, ch);
+    };
+    if constexpr (PIPE == 2) load_frags(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) {
+      const int b = ks % PIPE;
+      if constexpr (PIPE == 1) load_frags(ks, 0);
+      else if (ks + 1 < kKSteps) load_frags(ks + 1, (ks + 1) % PIPE);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) mma(acc[i][j], af[i], bfr[j], Elt{});
-      extra(s, kt * kKSteps + ks, ch, af);
-      if (ADN + BDN > 0 && do_dma && ks < kDmaSteps) {
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], af[b][i], bfr[b][j], Elt{});
+      extra.compute(xf[b], kt * kKSteps + ks, af[b]);
+      if constexpr (D > 0) {
+        if (ks < kDmaSteps) {
 #pragma unroll
-        for (int j = 0; j < kDmaPerStep; ++j) dma_one(ks * kDmaPerStep + j, kt + NS - 1, (kt + NS - 1) % NS);
+          for (int j = 0; j < kDmaPerStep; ++j)
+            dma_one(ks * kDmaPerStep + j, ktd, sd);
+        }
+        // no later load may be scheduled above the DMA: the vmcnt bounds count
+        // the loads issued after it
+        __builtin_amdgcn_sched_barrier(0);
       }
-      if (AP + BP > 0 && stash && ks >= kKSteps - kStashSteps) {
-        const int c0 = (ks - (kKSteps - kStashSteps)) * kPerStep;
+      if constexpr (AP + BP > 0) {
+        if (ks >= kKSteps - kStashSteps) {
+          const int c0 = (ks - (kKSteps - kStashSteps)) * kPerStep;
 #pragma unroll
-        for (int c = 0; c < kPerStep; ++c) stash_chunk(c0 + c, sa, sb, so);
+          for (int c = 0; c < kPerStep; ++c) stash_chunk(c0 + c, sa, sb, so);
 #pragma unroll
-        for (int c = 0; c < kPerStep; ++c) {
-          const int cc = c0 + c;
-          if (cc < AP ? refill_a : refill_b)
-            refill_chunk(cc, cc < AP ? kt + 1 + PFA : kt + 1 + PFB, sa, sb);
+          for (int c = 0; c < kPerStep; ++c) refill_chunk(c0 + c, kta, ktb, sa, sb);
         }
       }
     }
+    // tile kt + 1 must be in LDS: its DMA and this wave's LDS stores. A ring-only
+    // wave waits for its LDS stores alone (the compiler waited for the ring
+    // registers it stored).
+    if constexpr (ROLE == 1) wait_vm_lds<63>();
+    else wait_vm_lds<kVmAfter>();
+    lds_barrier();
   };
 
   // prologue: tile 0 complete in stage 0; DMA tiles 1 .. NS-2; ring tiles
@@ -384,42 +439,49 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
   fetch_a(0, 0);
   fetch_b(0, 0);
   dma(0, 0);
+  __builtin_amdgcn_sched_barrier(0);   // the ring fetches below stay after the DMA
 #pragma unroll
   for (int c = 0; c < AP + BP; ++c) stash_chunk(c, 0, 0, smem);
 #pragma unroll
-  for (int t = 1; t <= NS - 2; ++t)
-    if (t < nkt) dma(t, t);
+  for (int t = 1; t <= NS - 2; ++t) dma(cmin_dev(t, nkt - 1), t);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 1; p <= PFA; ++p)
-    if (AP > 0 && p < nkt) fetch_a(p, p % PFA);
+    if constexpr (AP > 0) fetch_a(cmin_dev(p, nkt - 1), p % PFA);
 #pragma unroll
   for (int p = 1; p <= PFB; ++p)
-    if (BP > 0 && p < nkt) fetch_b(p, p % PFB);
-  // loads issued after tile 0's DMA: the DMA of tiles 1 .. NS-2 and the ring
-  // fetches; count only what is certainly there (a smaller count waits longer)
-  if (nkt > NS + PFA) wait_vm_lds<(NS - 2) * D + PFA * FA + PFB * FB>();
-  else wait_vm_lds<0>();
+    if constexpr (BP > 0) fetch_b(cmin_dev(p, nkt - 1), p % PFB);
+  if constexpr (ROLE == 1) wait_vm_lds<63>();
+  else wait_vm_lds<(NS - 2) * D + PFA * FA + PFB * FB>();
   lds_barrier();
 
-  for (int k0 = 0; k0 < nkt; k0 += PFA) {
+  // ring slots of tile kt + 1 (k0 is a multiple of PFA, hence of PFB)
+  int k0 = 0;
+  for (; k0 + PFA <= nkt; k0 += PFA) {
 #pragma unroll
-    for (int p = 0; p < PFA; ++p) {
-      const int kt = k0 + p;
-      if (kt < nkt) {
-        // ring slots of tile kt + 1 (k0 is a multiple of PFA, hence of PFB)
-        const int sa = (p + 1) % PFA, sb = (p + 1) % PFB;
-        // stage (kt + NS - 1) % NS held tile kt - 1, which every wave finished
-        // reading before the barrier that ended the previous iteration
-        extra.tile_begin(kt, acc);
-        compute(kt, sa, sb);
-        if (kt + 1 < nkt) {
-          // tile kt + 1 must be in LDS: its DMA and this wave's LDS stores
-          if (kt + NS + PFA + 1 < nkt) wait_vm_lds<kVmAfter>();
-          else wait_vm_lds<0>();
-        }
-        lds_barrier();
-      }
-    }
+    for (int p = 0; p < PFA; ++p) iteration(k0 + p, (p + 1) % PFA, (p + 1) % PFB);
+  }
+#pragma unroll
+  for (int p = 0; p + 1 < PFA; ++p)
+    if (k0 + p < nkt) iteration(k0 + p, (p + 1) % PFA, (p + 1) % PFB);
+  // the refetches of the last tile land before the caller reuses the LDS
+  wait_vm_lds<0>();
+  lds_barrier();
+}
+
+template <class TL, class Elt, class ALoad, class BLoad, class Extra>
+__device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], const ALoad& aload,
+                                              const BLoad& bload, int nkt, u32x4* smem,
+                                              Extra& extra) {
+  if constexpr (TL::WA > 0) {
+    // vmcnt counts one wave's loads, which complete in issue order: a wave that
+    // waited for a one-tile-deep DMA would also wait for every ring load issued
+    // before it. Split by wave, the ring keeps PFA tiles in flight.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wave < TL::WA) gemm_mainloop_role<1, TL, Elt>(acc, aload, bload, nkt, smem, extra);
+    else gemm_mainloop_role<2, TL, Elt>(acc, aload, bload, nkt, smem, extra);
+  } else {
+    gemm_mainloop_role<0, TL, Elt>(acc, aload, bload, nkt, smem, extra);
   }
 }
 
@@ -634,6 +696,16 @@ template <int CTRL>
 __device__ __forceinline__ void dpp_add_step(float& v) {
   v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
+// Sum over each half-wave (lanes 0-31, 32-63), left in lanes 31 and 63: DPP
+// butterflies within 16-lane rows (xor 1, xor 2, half-row and row mirrors), then
+// row_bcast:15 adds row 0's (row 2's) lane 15 into row 1 (row 3).
+__device__ __forceinline__ float half_wave_sum(float v) {
+  dpp_add_step<0xb1>(v);    // quad_perm [1,0,3,2]
+  dpp_add_step<0x4e>(v);    // quad_perm [2,3,0,1]
+  dpp_add_step<0x141>(v);   // row_half_mirror
+  dpp_add_step<0x140>(v);   // row_mirror
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
+}
 template <int G>
 __device__ __forceinline__ void group_sum(float& v) {
   if constexpr (G >= 2) dpp_add_step<0xb1>(v);
@@ -670,7 +742,9 @@ struct RouterExtra {
   f32x16 racc[FM][RT];
   int wave, lane, brow0;   // brow0: LDS row of router column 0
   __device__ __forceinline__ void init(int w, int l, int r0) {
-    wave = w;
+    // wave-uniform in a scalar register: the K-step test below is then a scalar
+    // branch around the MFMAs (they would run with an empty EXEC mask too)
+    wave = __builtin_amdgcn_readfirstlane(w);
     lane = l;
     brow0 = r0;
 #pragma unroll
@@ -678,16 +752,24 @@ struct RouterExtra {
 #pragma unroll
       for (int j = 0; j < RT; ++j) racc[i][j] = zero16();
   }
-  template <class AF>
-  __device__ __forceinline__ void operator()(const u32x4* s, int kstep, int ch, const AF& af) {
+  struct Frag {
+    u32x4 b[RT];
+  };
+  __device__ __forceinline__ void load(Frag& f, const u32x4* s, int kstep, int ch) const {
     if (kSplitK && (kstep % NW) != wave) return;
 #pragma unroll
     for (int j = 0; j < RT; ++j) {
       const int col0 = (kSplitK ? j : wave * RT + j) * 32;
-      const u32x4 b = s[lds_slot(brow0 + col0 + (lane & 31), ch)];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) mma(racc[i][j], af[i], b, Elt{});
+      f.b[j] = s[lds_slot(brow0 + col0 + (lane & 31), ch)];
     }
+  }
+  template <class AF>
+  __device__ __forceinline__ void compute(const Frag& f, int kstep, const AF& af) {
+    if (kSplitK && (kstep % NW) != wave) return;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) mma(racc[i][j], af[i], f.b[j], Elt{});
   }
   template <class ACC>
   __device__ __forceinline__ void tile_begin(int, ACC&) const {}
@@ -700,9 +782,10 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   constexpr int EP = 32 * NR;
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;   // waves across the z columns
   constexpr int NWT = NW * WMF;                      // all waves (WMF row groups)
-  // x streams from HBM once: a register ring holds PFA of its K tiles. The
-  // weight rows come from L2 by DMA into LDS, shared by the WMF row groups.
-  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true> TL;
+  // x streams from HBM once: a register ring of PFA K tiles, run by half of the
+  // waves. The weight rows come from L2 by DMA into LDS (the other half), shared
+  // by the WMF row groups.
+  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
   constexpr int FM = TL::FM;   // a wave covers the BM / WMF rows of its group
   typedef RouterExtra<Elt, FM, NR, NW> RX;
   // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
@@ -759,7 +842,8 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   }
 
   // -- RMSNorm row sums of squares ------------------------------------------
-  // lanes l and l ^ m (m < 32) hold the same rows
+  // the 32 lanes of each half-wave hold the same rows; their sum lands in lanes
+  // 31 and 63
   float ss[FM][16];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -768,11 +852,9 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
       float v = 0.f;
 #pragma unroll
       for (int j = 0; j < TL::FN; ++j) v += acc[i][j][e] * acc[i][j][e];
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off);
-      ss[i][e] = v;
+      ss[i][e] = half_wave_sum(v);
     }
-  if ((lane & 31) == 0) {
+  if ((lane & 31) == 31) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -937,8 +1019,10 @@ struct CoreRescale {
     for (int j = 0; j < FN; ++j)
       nxt[j] = (cs && r1 > 1 && colbase + 32 * j < r2) ? cs[colbase + 32 * j] : 1.f;
   }
+  struct Frag {};
+  __device__ __forceinline__ void load(Frag&, const u32x4*, int, int) const {}
   template <class AF>
-  __device__ __forceinline__ void operator()(const u32x4*, int, int, const AF&) const {}
+  __device__ __forceinline__ void compute(const Frag&, int, const AF&) const {}
   template <class ACC>
   __device__ __forceinline__ void tile_begin(int kt, ACC& acc) {
     if (!cs || kt == 0 || kt % tiles_per_r != 0) return;
@@ -962,7 +1046,9 @@ struct CoreRescale {
 template <class Elt, int BM, int BN, int WM, int WN, int PFA>
 __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
   typedef typename Elt::T T;
-  typedef Tile<BM, BN, 0, WM, WN, PFA, 1, 2, false, true> TL;
+  // half of the waves form c (x) z through the register ring, the other half
+  // issue the core^T DMA
+  typedef Tile<BM, BN, 0, WM, WN, PFA, 1, 2, false, true, WM * WN / 2> TL;
   __shared__ u32x4 smem[cmax(TL::kLdsBytes, TileStage<TL, T>::kBytes) / 16];
 
   const int ntn = (int)((a.r2 + BN - 1) / BN);
