@@ -137,6 +137,11 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     return fail(TMOE_EUNSUPPORTED, "top_k=%lld: at most %d", (long long)s.k, tmoe::kMaxTopK);
   if (s.r1 > 64)
     return fail(TMOE_EUNSUPPORTED, "r1=%lld: at most 64", (long long)s.r1);
+  // a GEMM tile (at most 512 operand rows of at most 4 MB) spans < 4 GB: the
+  // kernels address it with 32-bit offsets
+  if (s.d_in > (1 << 20) || s.r2 > (1 << 20))
+    return fail(TMOE_EUNSUPPORTED, "d_in=%lld, r2=%lld: at most %d each", (long long)s.d_in,
+                (long long)s.r2, 1 << 20);
 
   tmoe_plan* p = new (std::nothrow) tmoe_plan();
   if (!p) return fail(TMOE_EINVAL, "out of host memory");

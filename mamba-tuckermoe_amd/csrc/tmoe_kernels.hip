@@ -1,4 +1,6 @@
 // Launch configurations of the gfx950 kernels (device code: tmoe_kernels.hpp).
+#include <atomic>
+
 #include "tmoe_kernels.hpp"
 #include "tmoe_small.hpp"
 
@@ -71,6 +73,30 @@ hipError_t launch_outproj_t(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device id).
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// bf16 out-projection: persistent, one work-group per compute unit (its LDS
+// holds one), each looping over the tiles b, b + grid, ...
+hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
+  typedef OutCfgBF16 C;
+  const int64_t tiles = (int64_t)cdiv(a.T, C::BM) * cdiv(a.d_out, C::BN);
+  const int64_t ncu = cu_count();
+  const dim3 grid((unsigned)(tiles < ncu ? tiles : ncu)), block(64 * C::WM * C::WN);
+  hipLaunchKernelGGL((dev::k_outproj_pp<C::BM, C::BN, C::WM, C::WN>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 // small-T path: 16-column work-groups of kSkW waves over blocks of 16 MF tokens
 constexpr int kSkW = 16;
 
@@ -135,7 +161,7 @@ hipError_t launch_core(const FwdArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t st) {
-  return a.dtype == kDtypeBF16 ? launch_outproj_t<EltBF16, OutCfgBF16>(a, st)
+  return a.dtype == kDtypeBF16 ? launch_outproj_bf16(a, st)
                                : launch_outproj_t<EltF32, OutCfgF32>(a, st);
 }
 

@@ -93,7 +93,9 @@ __device__ __forceinline__ f32x16 zero16() {
 // is written to LDS. Splitting the two lets loads for later K tiles stay in
 // flight while earlier ones are consumed. Rows past the operand's end are
 // clamped to its last row: their products only reach output rows/columns that
-// are never stored.
+// are never stored. A tile's rows span less than 4 GB (the plan bounds d_in and
+// r2), so offsets from the tile's first row are 32-bit: the base stays uniform
+// and a lane carries one 32-bit offset per load.
 
 struct RowLoader {          // plain row-major, K-contiguous operand
   typedef u32x4 Raw;
@@ -103,7 +105,7 @@ struct RowLoader {          // plain row-major, K-contiguous operand
   int rows_valid;           // >= 1
   __device__ __forceinline__ const char* gaddr(int row, int ch, int kt) const {
     const int r = row < rows_valid ? row : rows_valid - 1;
-    return base + (int64_t)r * row_bytes + kt * kTileKBytes + ch * 16;
+    return base + ((uint32_t)r * (uint32_t)row_bytes + (uint32_t)(kt * kTileKBytes + ch * 16));
   }
   __device__ __forceinline__ Raw fetch(int row, int ch, int kt) const {
     return *reinterpret_cast<const u32x4*>(gaddr(row, ch, kt));
@@ -203,6 +205,13 @@ __device__ __forceinline__ void wait_vm_lds() {
   static_assert(VM >= 0 && VM < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
 }
+
+// 24 wait states: more than the longest MFMA result latency a following VALU,
+// LDS or memory instruction must respect (16-pass fp32 MFMAs need 18 or 19).
+// Issued at the end of every main-loop K tile: the last MFMAs may sit in a
+// conditional block, and the compiler's own padding before the copies it makes
+// of the accumulators at the loop exit was found one wait state short there.
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 
 // Work-group barrier that orders LDS traffic only; loads still in flight stay in
 // flight. The empty asm statements keep the compiler from moving memory
@@ -426,6 +435,9 @@ __device__ __forceinline__ void gemm_mainloop_role(f32x16 (&acc)[TL::FM][TL::FN]
         }
       }
     }
+    // the accumulators may be copied at the loop exit right after a skipped
+    // conditional MFMA block
+    mfma_drain();
     // tile kt + 1 must be in LDS: its DMA and this wave's LDS stores. A ring-only
     // wave waits for its LDS stores alone (the compiler waited for the ring
     // registers it stored).
@@ -498,6 +510,11 @@ __device__ __forceinline__ void gemm_mainloop(f32x16 (&acc)[TL::FM][TL::FN], con
 // reader (group 1, phase 2kt - 1) waited for its LDS reads before barrier
 // 2kt - 1; group 0 waits for the DMA at the end of phase 2kt + 1, before either
 // group reads tile kt + 1.
+// Group 0 issues every DMA, tile 0's included, and group 1 never waits on vmcnt:
+// stores group 1 issued before the call keep draining while it runs.
+// The MFMAs take B as their first operand, so acc[i][j] holds the transposed
+// block: lane l has row l & 31 of row block i and, in elements 4q .. 4q + 3,
+// columns 8q + 4 (l >> 5) .. + 3 of column block j (stage_tile_t).
 template <class TL, class Elt, class ALoad, class BLoad>
 __device__ __forceinline__ void gemm_mainloop_pingpong(f32x16 (&acc)[TL::FM][TL::FN],
                                                        const ALoad& aload, const BLoad& bload,
@@ -532,9 +549,11 @@ __device__ __forceinline__ void gemm_mainloop_pingpong(f32x16 (&acc)[TL::FM][TL:
           (lds_vptr)(s + (kARows + (blk - kABlk) * 8) * 8), 16, 0, 0);
   };
 
-  // prologue: tile 0 by all eight waves
-  for (int blk = wave; blk < kABlk + kBBlk; blk += 8) dma_block(blk, 0, 0);
-  wait_vm_lds<0>();
+  // prologue: tile 0 by group 0
+  if (grp == 0) {
+    for (int blk = wave; blk < kABlk + kBBlk; blk += 4) dma_block(blk, 0, 0);
+    wait_vm_lds<0>();
+  }
   lds_barrier();
   if (grp == 1) lds_barrier();
 
@@ -564,23 +583,27 @@ __device__ __forceinline__ void gemm_mainloop_pingpong(f32x16 (&acc)[TL::FM][TL:
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) mma(acc[i][j], af[ks][i], bfr[ks][j], Elt{});
+        for (int j = 0; j < FN; ++j) mma(acc[i][j], bfr[ks][j], af[ks][i], Elt{});
     if (grp == 0) wait_vm_lds<0>();   // DMA of tile kt + 1 has landed
     lds_barrier();
   }
   if (grp == 0) lds_barrier();
+  mfma_drain();
 }
 
 // Work-group -> tile order for 2-D grids launched as 1-D. Consecutive
 // work-groups land on different XCDs (round robin over 8); this hands each XCD a
 // contiguous run of tiles, row-major over (m, n), so the A rows of an m tile are
 // fetched into one XCD's L2 and reused for all its n tiles.
-__device__ __forceinline__ void tile_coords(int n_tiles_n, int n_tiles, int& tm, int& tn) {
-  const int b = blockIdx.x;
+__device__ __forceinline__ void tile_coords_of(int b, int n_tiles_n, int n_tiles, int& tm,
+                                               int& tn) {
   const int per = n_tiles / 8;
   const int t = b < per * 8 ? (b % 8) * per + b / 8 : b;
   tm = t / n_tiles_n;
   tn = t - tm * n_tiles_n;
+}
+__device__ __forceinline__ void tile_coords(int n_tiles_n, int n_tiles, int& tm, int& tn) {
+  tile_coords_of(blockIdx.x, n_tiles_n, n_tiles, tm, tn);
 }
 
 // ---- C tile store through LDS ----------------------------------------------
@@ -630,6 +653,55 @@ __device__ __forceinline__ void flush_tile(const char* stage, T* dst, int64_t ld
   constexpr int CPR = TL::BN * (int)sizeof(T) / 16;   // chunks per row
   constexpr int EPC = 16 / (int)sizeof(T);           // elements per chunk
   for (int c = threadIdx.x; c < TL::BM * CPR; c += TL::kThreads) {
+    const int row = c / CPR, ch = c - row * CPR;
+    if (row < rows_valid && ch * EPC < cols_valid)
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + row * RB + ch * 16),
+                                  reinterpret_cast<u32x4*>(dst + row * ld + ch * EPC));
+  }
+}
+
+// Stages a bf16 tile from transposed accumulators (gemm_mainloop_pingpong): a
+// lane's elements 4q .. 4q + 3 of block (i, j) are four consecutive columns of
+// one row, stored as one 8-byte LDS write of (acc * scale + bias). Columns are
+// cut at multiples of 16 only, so a group of four is wholly valid or not. bias
+// and scale point at the tile's first column and are 16-byte aligned.
+template <class TL>
+__device__ __forceinline__ void stage_tile_t(const f32x16 (&acc)[TL::FM][TL::FN], char* stage,
+                                             const float* bias, const float* scale, int cols_valid) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
+  constexpr int RB = TileStage<TL, uint16_t>::kRowBytes;
+#pragma unroll
+  for (int j = 0; j < TL::FN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = wn * TL::kWaveN + j * 32 + 8 * q + 4 * (lane >> 5);
+      // columns past the end read column 0 (16-byte aligned); they are not stored
+      const int cc = col < cols_valid ? col : 0;
+      const float4 bv = *reinterpret_cast<const float4*>(bias + cc);
+      const float4 sv = scale ? *reinterpret_cast<const float4*>(scale + cc)
+                              : float4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+      for (int i = 0; i < TL::FM; ++i) {
+        const int row = wm * TL::kWaveM + i * 32 + (lane & 31);
+        uint2 v;
+        v.x = pack_bf16x2(acc[i][j][4 * q] * sv.x + bv.x, acc[i][j][4 * q + 1] * sv.y + bv.y);
+        v.y = pack_bf16x2(acc[i][j][4 * q + 2] * sv.z + bv.z,
+                          acc[i][j][4 * q + 3] * sv.w + bv.w);
+        *reinterpret_cast<uint2*>(stage + row * RB + col * 2) = v;
+      }
+    }
+}
+
+// flush_tile by the NT threads t0 .. t0 + NT - 1 of the work-group (tid: this
+// thread's index among them).
+template <class TL, class T, int NT>
+__device__ __forceinline__ void flush_tile_by(const char* stage, T* dst, int64_t ld, int rows_valid,
+                                              int cols_valid, int tid) {
+  constexpr int RB = TileStage<TL, T>::kRowBytes;
+  constexpr int CPR = TL::BN * (int)sizeof(T) / 16;
+  constexpr int EPC = 16 / (int)sizeof(T);
+  for (int c = tid; c < TL::BM * CPR; c += NT) {
     const int row = c / CPR, ch = c - row * CPR;
     if (row < rows_valid && ch * EPC < cols_valid)
       __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + row * RB + ch * 16),
@@ -1107,12 +1179,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
   RowLoader bl{reinterpret_cast<const char*>(a.uoutT) + n0 * row_bytes, row_bytes,
                (int)(a.d_out - n0)};
   f32x16 acc[TL::FM][TL::FN];
-  if constexpr (TL::kThreads == 512 && NS == 2) {
-    gemm_mainloop_pingpong<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem);
-  } else {
-    NoExtra nx;
-    gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, nx);
-  }
+  NoExtra nx;
+  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, nx);
 
   char* stage = reinterpret_cast<char*>(smem);
   const int cols_valid = (int)(a.d_out - n0);
@@ -1130,6 +1198,45 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
   __syncthreads();
   flush_tile<TL, T>(stage, reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0, a.d_out, rows_valid,
                     cols_valid);
+}
+
+// Persistent bf16 out-projection (8 waves, ping-pong main loop): work-group b
+// takes tiles b, b + gridDim.x, ... Each tile is staged in LDS by all waves and
+// written out by group 1 alone, whose stores then drain during the next tile's
+// main loop (group 1 never waits on vmcnt; group 0 issues every DMA).
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
+  typedef uint16_t T;
+  typedef Tile<BM, BN, 0, WM, WN, 1, 1, 2, true, true> TL;
+  static_assert(TL::kThreads == 512, "ping-pong: 8 waves");
+  __shared__ u32x4 smem[cmax(TL::kLdsBytes, TileStage<TL, T>::kBytes) / 16];
+  const int ntn = (int)((a.d_out + BN - 1) / BN);
+  const int ntm = (int)((a.T + BM - 1) / BM);
+  const int ntiles = ntm * ntn;
+  const int grp = (threadIdx.x >> 6) >> 2;
+  const int64_t row_bytes = a.r2 * (int64_t)sizeof(T);
+  char* stage = reinterpret_cast<char*>(smem);
+  for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    int tm, tn;
+    tile_coords_of(t, ntn, ntiles, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM;
+    const int64_t n0 = (int64_t)tn * BN;
+    const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+    const int cols_valid = (int)(a.d_out - n0);
+    RowLoader al{reinterpret_cast<const char*>(a.mid) + m0 * row_bytes, row_bytes, rows_valid};
+    RowLoader bl{reinterpret_cast<const char*>(a.uoutT) + n0 * row_bytes, row_bytes, cols_valid};
+    f32x16 acc[TL::FM][TL::FN];
+    gemm_mainloop_pingpong<TL, EltBF16>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem);
+    stage_tile_t<TL>(acc, stage, a.bias + n0, a.out_scale ? a.out_scale + n0 : nullptr,
+                     cols_valid);
+    wait_vm_lds<63>();   // LDS writes done; stores of the previous tile may still drain
+    lds_barrier();
+    if (grp == 1)
+      flush_tile_by<TL, T, 256>(stage, reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0, a.d_out,
+                                rows_valid, cols_valid, (int)threadIdx.x - 256);
+    wait_vm_lds<63>();   // the staged tile is read before the next tile's DMA reuses it
+    lds_barrier();
+  }
 }
 
 // ---- packing kernels -----------------------------------------------------

@@ -149,6 +149,7 @@ __device__ __forceinline__ void skinny_tile(const ASrc& asrc, const char* b, int
       }
     }
   }
+  mfma_drain();   // the last MFMAs sit in a conditional block
   if (rank_len == 0) {
 #pragma unroll
     for (int f = 0; f < MF; ++f) tot[f] = acc[f];
