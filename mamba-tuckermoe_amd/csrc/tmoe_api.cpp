@@ -28,6 +28,8 @@ struct tmoe_plan {
   // add the U_in column scales, the core scale table and the U_out column scales.
   size_t off_front, off_router, off_gain, off_uexp, off_core, off_uout, off_bias;
   size_t off_sin, off_cscale, off_sout, off_craw, packed_bytes;
+  bool core_p;      // the core runs k_core_pp (T > kSmallT) from P^T at off_core_p
+  size_t off_core_p;
 };
 
 namespace {
@@ -79,11 +81,14 @@ struct Layout {
 Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   Layout L{};
   size_t o = 0;
+  // k_core_pp reads c and stores mid in whole 256-token tiles
+  const int64_t tile_rows =
+      p->core_p ? (T + tmoe::kCorePRows - 1) / tmoe::kCorePRows * tmoe::kCorePRows : T;
   L.z = o;   o = align256(o + (size_t)T * p->s.r3 * p->es);
-  L.c = o;   o = align256(o + (size_t)T * p->s.r1 * sizeof(float));
+  L.c = o;   o = align256(o + (size_t)tile_rows * p->s.r1 * sizeof(float));
   L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
   L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
-  L.mid = o; o = align256(o + (size_t)T * p->s.r2 * p->es);
+  L.mid = o; o = align256(o + (size_t)tile_rows * p->s.r2 * p->es);
   L.raw = o;
   if (T <= tmoe::kSmallT) o = align256(o + (size_t)T * (p->s.r3 + p->s.E) * sizeof(float));
   L.total = o;
@@ -168,6 +173,9 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     p->off_sout = o;   o = align256(o + (size_t)s.d_out * sizeof(float));
     p->off_craw = o;   o = align256(o + (size_t)s.r1 * s.r2 * sizeof(float));
   }
+  p->core_p = tmoe::core_p_supported(s.r1, s.r2, p->kdtype == TMOE_BF16, p->fp8w);
+  p->off_core_p = 0;
+  if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)s.r1 * s.r2 * s.r3 * p->es); }
   p->packed_bytes = o;
   *plan_out = p;
   return TMOE_OK;
@@ -217,6 +225,11 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
   if ((e = tmoe::launch_transpose(core, base + p->off_core, s.r1 * s.r3, s.r2, es, st)) !=
       hipSuccess)
     return hip_fail(e, "pack core");
+  if (p->core_p &&
+      (e = tmoe::launch_pack_core_p(core, false, nullptr,
+                                    reinterpret_cast<uint16_t*>(base + p->off_core_p), s.r1, s.r3,
+                                    s.r2, st)) != hipSuccess)
+    return hip_fail(e, "pack core (P layout)");
   if ((e = tmoe::launch_transpose(U_out, base + p->off_uout, s.r2, s.d_out, es, st)) !=
       hipSuccess)
     return hip_fail(e, "pack U_out");
@@ -267,6 +280,10 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
   if ((e = tmoe::launch_core_scales(core_scale, f32at(p->off_cscale), s.r1, s.r2, st)) !=
       hipSuccess)
     return hip_fail(e, "pack core scales");
+  if (p->core_p &&
+      (e = tmoe::launch_pack_core_p(core_q, true, core_scale, bf16at(p->off_core_p), s.r1, s.r3,
+                                    s.r2, st)) != hipSuccess)
+    return hip_fail(e, "pack core (P layout)");
   if ((e = tmoe::launch_transpose_e4m3(U_out_q, bf16at(p->off_uout), s.r2, s.d_out, nullptr, 1,
                                        st)) != hipSuccess)
     return hip_fail(e, "pack U_out");
@@ -317,6 +334,7 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
   a.uexp = reinterpret_cast<const float*>(pk + p->off_uexp);
   a.coreT = pk + p->off_core;
+  a.coreP = p->core_p ? pk + p->off_core_p : nullptr;
   a.uoutT = pk + p->off_uout;
   a.bias = reinterpret_cast<const float*>(pk + p->off_bias);
   if (p->fp8w) {

@@ -31,6 +31,9 @@ struct FwdArgs {
   const float* gain;            // (r3)                 inner_norm.weight
   const float* uexp;            // (E, r1)              U_expert
   const void* coreT;            // (r2, r1*r3)          core as (r1*r3, r2), transposed
+  const void* coreP;            // (r1*r2, r3)          k_core_pp's P^T: row (qb*r1 + r)*32 + qq
+                                //                      = channel (r, 32 qb + qq); null when
+                                //                      the plan does not use k_core_pp
   const void* uoutT;            // (d_out, r2)          U_out transposed
   const float* bias;            // (d_out)
   // fp8-weight plans only (null otherwise): per-output-channel scales
@@ -52,6 +55,17 @@ struct FwdArgs {
 // Token counts up to kSmallT take the small-T path (tmoe_small.hpp).
 constexpr int64_t kSmallT = 256;
 
+// k_core_pp (the persistent core for bf16 plans): ranks r1 in {1, 2, 4}, r1 * r2 a
+// multiple of its 256-row tiles, and for fp8 weights at most kCorePScales channel
+// scales (staged in LDS). Its 256-token tiles store whole tiles of mid, so the
+// workspace holds mid for T rounded up to kCorePRows rows.
+constexpr int kCorePRows = 256;
+constexpr int64_t kCorePScales = 4096;
+inline bool core_p_supported(int64_t r1, int64_t r2, bool bf16, bool fp8w) {
+  return bf16 && (r1 == 1 || r1 == 2 || r1 == 4) && (r1 * r2) % 256 == 0 &&
+         (!fp8w || r1 * r2 <= kCorePScales);
+}
+
 // Each launcher enqueues one kernel on `stream` and returns hipGetLastError().
 hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
@@ -66,6 +80,10 @@ hipError_t launch_small_out(const FwdArgs& a, hipStream_t stream);
 // scale colscale[(row / group) * cols + col] is zero are stored as zero.
 hipError_t launch_transpose_e4m3(const uint8_t* src, uint16_t* dst, int64_t rows, int64_t cols,
                                  const float* colscale, int64_t group, hipStream_t stream);
+// k_core_pp's P^T (r1*r2, r3) from core (r1, r3, r2): bf16 bits, or e4m3 codes with
+// channel scales sc (r1, r2) (null for bf16; a zero scale packs its channel as zeros).
+hipError_t launch_pack_core_p(const void* core, bool e4m3, const float* sc, uint16_t* dst,
+                              int64_t r1, int64_t r3, int64_t r2, hipStream_t stream);
 // core scale table (r1, r2) from the per-channel scales sc (r1, r2)
 hipError_t launch_core_scales(const float* sc, float* cs, int64_t r1, int64_t r2,
                               hipStream_t stream);

@@ -11,6 +11,9 @@ using dev::EltBF16;
 using dev::EltF32;
 
 constexpr int kDtypeBF16 = 1;   // TMOE_BF16
+// K steps per ping-pong phase of k_core_pp: 2 keeps its fragments in 236 VGPRs
+// (4 spills past the 256 of a two-wave-per-SIMD launch)
+constexpr int kCorePSteps = 2;
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
@@ -58,6 +61,10 @@ hipError_t launch_front_t(const FwdArgs& a, hipStream_t st) {
   }
 }
 
+// Persistent core: one work-group per compute unit, at most one per tile.
+template <int R1>
+hipError_t launch_core_pp_r(const FwdArgs& a, hipStream_t st);
+
 template <class Elt, class C>
 hipError_t launch_core_t(const FwdArgs& a, hipStream_t st) {
   const dim3 grid(cdiv(a.T, C::BM) * cdiv(a.r2, C::BN)), block(64 * C::WM * C::WN);
@@ -94,6 +101,15 @@ hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
   const int64_t ncu = cu_count();
   const dim3 grid((unsigned)(tiles < ncu ? tiles : ncu)), block(64 * C::WM * C::WN);
   hipLaunchKernelGGL((dev::k_outproj_pp<C::BM, C::BN, C::WM, C::WN>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+template <int R1>
+hipError_t launch_core_pp_r(const FwdArgs& a, hipStream_t st) {
+  const int64_t tiles = (int64_t)cdiv(a.T, kCorePRows) * (a.r1 * a.r2 / 256);
+  const int64_t ncu = cu_count();
+  const dim3 grid((unsigned)(tiles < ncu ? tiles : ncu)), block(512);
+  hipLaunchKernelGGL((dev::k_core_pp<R1, kCorePSteps>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
@@ -156,8 +172,27 @@ hipError_t launch_front(const FwdArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_core(const FwdArgs& a, hipStream_t st) {
+  if (a.dtype == kDtypeBF16 && a.coreP) {
+    switch (a.r1) {
+      case 1: return launch_core_pp_r<1>(a, st);
+      case 2: return launch_core_pp_r<2>(a, st);
+      case 4: return launch_core_pp_r<4>(a, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   return a.dtype == kDtypeBF16 ? launch_core_t<EltBF16, CoreCfgBF16>(a, st)
                                : launch_core_t<EltF32, CoreCfgF32>(a, st);
+}
+
+hipError_t launch_pack_core_p(const void* core, bool e4m3, const float* sc, uint16_t* dst,
+                              int64_t r1, int64_t r3, int64_t r2, hipStream_t st) {
+  if (r1 == 0 || r2 == 0 || r3 == 0) return hipSuccess;
+  const dim3 grid(cdiv(r2, 32), cdiv(r3, 32), (unsigned)r1), block(256);
+  if (e4m3)
+    hipLaunchKernelGGL(dev::k_pack_core_p<true>, grid, block, 0, st, core, dst, r1, r3, r2, sc);
+  else
+    hipLaunchKernelGGL(dev::k_pack_core_p<false>, grid, block, 0, st, core, dst, r1, r3, r2, sc);
+  return hipGetLastError();
 }
 
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t st) {

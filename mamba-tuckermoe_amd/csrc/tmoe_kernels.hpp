@@ -24,6 +24,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "tmoe_internal.h"
 
 namespace tmoe {
@@ -1159,6 +1161,218 @@ __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
                     (int)(a.r2 - n0));
 }
 
+// ---- k_core_pp: mid = sum_r c_r (z P_r), persistent ping-pong  (model.py:87-98)
+// The north star's form of the core: one GEMM Y = z P with K = r3, where P is
+// core viewed as (r3, r1 * r2), fused with the weighted reduction over r1:
+//   mid[t, q] = sum_r c[t, r] * sc[r, q] * Y[t, (r, q)]      (sc = 1 without fp8)
+// P^T is packed with its rows in blocks of 32 output channels q, each block
+// holding the R1 ranks in turn (row (qb * R1 + r) * 32 + qq = channel
+// (r, 32 qb + qq)), so the R1 column blocks a wave owns for one group of 32
+// channels hold the same (row, q) in the same lane and the reduction over r is
+// elementwise over accumulators. Both operands arrive by DMA.
+//
+// 256 x 256 tiles (256 tokens x 256 / R1 channels), 8 waves as 4 x 2, each wave
+// 64 rows x 4 column blocks (QG = 4 / R1 channel groups). The work-group runs
+// its tiles b, b + grid, ... as one stream of K tiles (r3 / 64 per tile) through
+// the two-group ping-pong of gemm_mainloop_pingpong, so the DMA never stops at a
+// tile boundary: after the compute phase of a tile's last K tile each wave
+// reduces its accumulators over r and stores its part of mid straight from
+// registers (8 bytes a lane; group 0, the DMA issuer, after its wait for the
+// next K tile), then starts the next tile with zeroed
+// accumulators. SPP K steps of a K tile are read per memory phase (2: two
+// memory/compute phase pairs per K tile, which halves the fragment registers).
+// A tile's rows of c reach LDS by DMA with its first K tile (three buffers: the
+// second group still reads tile i - 1's while tile i + 1's lands), so the
+// epilogue issues no global load and waits on nothing. The stores are
+// unconditional: the workspace holds mid for whole 256-row tiles.
+template <int R1, int SPP>
+__global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
+  typedef Tile<256, 256, 0, 4, 2, 1, 1, 2, true, true> TL;
+  constexpr int FM = TL::FM, FN = TL::FN;   // 2 x 4 blocks of 32 x 32
+  static_assert(FN % R1 == 0, "rank blocks per wave");
+  constexpr int QG = FN / R1;               // channel groups of 32 per wave
+  constexpr int kKSteps = kTileKBytes / 32;
+  static_assert(kKSteps % SPP == 0, "steps per phase");
+  constexpr int kHalves = kKSteps / SPP;    // memory/compute phase pairs per K tile
+  constexpr int kABlk = TL::BM / 8, kBBlk = TL::BN / 8;
+  constexpr int kDmaPerWave = (kABlk + kBBlk) / 4;
+  constexpr int kScaleFloats = (int)kCorePScales;   // fp8 channel scales staged in LDS
+  constexpr int kCBuf = TL::BM * R1;                // floats of c per tile
+  constexpr int kCDma = kCBuf / 256;                // 1 KB DMA instructions per tile's c
+  static_assert(kCDma <= 4, "c DMA by group 0's waves");
+  __shared__ u32x4 smem[TL::kLdsBytes / 16 + kScaleFloats / 4 + 3 * kCBuf / 4];
+  float* sc_lds = reinterpret_cast<float*>(smem + TL::kLdsBytes / 16);
+  float* c_lds = sc_lds + kScaleFloats;   // [3][BM][R1]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
+  const int64_t r2 = a.r2, r3 = a.r3;
+  const int ntn = (int)(R1 * r2 / TL::BN);
+  const int ntm = (int)((a.T + TL::BM - 1) / TL::BM);
+  const int ntiles = ntm * ntn;
+  const int nkt = (int)(r3 * 2 / kTileKBytes);   // K tiles per output tile
+  const int my_tiles = ((int)blockIdx.x < ntiles) ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = my_tiles * nkt;
+  const int64_t row_bytes = r3 * 2;
+  const int kt_rot = ((int)blockIdx.x >> 3) % nkt;
+  const bool fp8 = a.core_scale_raw != nullptr;
+  if (fp8) {   // the plan bounds r1 * r2 by kScaleFloats for fp8 weights
+    for (int i = tid; i < R1 * (int)r2; i += 512) sc_lds[i] = a.core_scale_raw[i];
+  }
+
+  auto coords = [&](int i, int& tm, int& tn) __attribute__((always_inline)) {
+    tile_coords_of((int)blockIdx.x + i * (int)gridDim.x, ntn, ntiles, tm, tn);
+  };
+  // DMA of K tile g of this work-group's stream into `stage` (group 0's waves)
+  auto dma_g = [&](int g, int stage) __attribute__((always_inline)) {
+    int tm, tn;
+    coords(g / nkt, tm, tn);
+    // work-groups on one XCD start their tiles' K loops at different K tiles:
+    // they read the same P^T rows, and reading the same lines at the same moment
+    // measured 20% slower (the sum's order per output element is fixed per tile)
+    const int kt = (g % nkt + kt_rot) % nkt;
+    const int64_t m0 = (int64_t)tm * TL::BM;
+    const int rows_valid = (int)(a.T - m0 < TL::BM ? a.T - m0 : TL::BM);
+    RowLoader al{reinterpret_cast<const char*>(a.z) + m0 * row_bytes, row_bytes, rows_valid};
+    RowLoader bl{reinterpret_cast<const char*>(a.coreP) + (int64_t)tn * TL::BN * row_bytes,
+                 row_bytes, TL::BN};
+    if (g % nkt == 0 && wave < kCDma) {
+      // 16 bytes of the tile's c rows a lane; the workspace holds c for whole
+      // tiles (rows past T are never used for an output row below T)
+      const int i = g / nkt;
+      const int64_t f = (int64_t)wave * 256 + lane * 4;   // float index within the tile
+      __builtin_amdgcn_global_load_lds((gbl_cvptr)(a.c + m0 * R1 + f),
+                                       (lds_vptr)(c_lds + (i % 3) * kCBuf + wave * 256), 16, 0, 0);
+    }
+    u32x4* s = smem + stage * TL::kStage;
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int blk = wave + 4 * j;
+      const int lc = dma_chunk(lane, blk);   // kABlk is even: block parity is kept
+      if (blk < kABlk)
+        __builtin_amdgcn_global_load_lds((gbl_cvptr)al.gaddr(blk * 8 + (lane >> 3), lc, kt),
+                                         (lds_vptr)(s + blk * 64), 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(
+            (gbl_cvptr)bl.gaddr((blk - kABlk) * 8 + (lane >> 3), lc, kt),
+            (lds_vptr)(s + (TL::BM + (blk - kABlk) * 8) * 8), 16, 0, 0);
+    }
+  };
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = zero16();
+  if (total == 0) return;   // uniform over the work-group
+
+  // epilogue of tile i: mid[row, q] = sum_r c[row, r] sc[r, q] acc (transposed
+  // accumulators: lane l holds row l & 31 of block f and, in elements 4 u .. 4 u + 3,
+  // channels 8 u + 4 (l >> 5) .. + 3 of each column block)
+  auto epilogue = [&](int i, auto fp8_tag) __attribute__((always_inline)) {
+    constexpr bool kFp8 = decltype(fp8_tag)::value;
+    int tm, tn;
+    coords(i, tm, tn);
+    const int64_t m0 = (int64_t)tm * TL::BM;
+    float cf[FM][R1];
+#pragma unroll
+    for (int f = 0; f < FM; ++f)
+#pragma unroll
+      for (int r = 0; r < R1; ++r)
+        cf[f][r] = c_lds[(i % 3) * kCBuf + (wm * TL::kWaveM + 32 * f + (lane & 31)) * R1 + r];
+#pragma unroll
+    for (int g = 0; g < QG; ++g) {
+      // channel block of column blocks g * R1 .. g * R1 + R1 - 1 of this wave
+      const int qb = tn * (TL::BN / 32 / R1) + (wn * FN) / R1 + g;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = qb * 32 + 8 * u + 4 * (lane >> 5);
+        float sv[R1][4];
+#pragma unroll
+        for (int r = 0; r < R1; ++r)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sv[r][v] = kFp8 ? sc_lds[r * r2 + q + v] : 1.f;
+#pragma unroll
+        for (int f = 0; f < FM; ++f) {
+          const int64_t row = m0 + wm * TL::kWaveM + 32 * f + (lane & 31);
+          float o[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float sum = 0.f;
+#pragma unroll
+            for (int r = 0; r < R1; ++r) {
+              const float y = kFp8 ? acc[f][g * R1 + r][4 * u + v] * sv[r][v]
+                                   : acc[f][g * R1 + r][4 * u + v];
+              sum += cf[f][r] * y;
+            }
+            o[v] = sum;
+          }
+          uint2 pk;
+          pk.x = pack_bf16x2(o[0], o[1]);
+          pk.y = pack_bf16x2(o[2], o[3]);
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.mid) + row * r2 + q) = pk;
+        }
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < FM; ++f)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[f][j] = zero16();
+  };
+
+  // prologue: K tile 0 by group 0; group 1 starts one barrier late
+  if (grp == 0) {
+    dma_g(0, 0);
+    wait_vm_lds<0>();
+  }
+  __syncthreads();   // also publishes the staged scales
+  if (grp == 1) lds_barrier();
+
+  for (int g = 0; g < total; ++g) {
+    const u32x4* s = smem + (g & 1) * TL::kStage;
+    const bool last_kt = g % nkt == nkt - 1;
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) {
+      // -- memory phase: fragments of K steps h * SPP .. + SPP - 1 ------------
+      u32x4 af[SPP][FM], bfr[SPP][FN];
+#pragma unroll
+      for (int ks = 0; ks < SPP; ++ks) {
+        const int ch = (h * SPP + ks) * 2 + (lane >> 5);
+#pragma unroll
+        for (int f = 0; f < FM; ++f)
+          af[ks][f] = s[lds_slot(wm * TL::kWaveM + f * 32 + (lane & 31), ch)];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          bfr[ks][j] = s[lds_slot(TL::BM + wn * TL::kWaveN + j * 32 + (lane & 31), ch)];
+      }
+      if (h == 0 && grp == 0 && g + 1 < total) dma_g(g + 1, (g + 1) & 1);
+      wait_vm_lds<63>();   // this wave's fragment reads; the DMA stays in flight
+      lds_barrier();
+      // -- compute phase --------------------------------------------------------
+#pragma unroll
+      for (int ks = 0; ks < SPP; ++ks)
+#pragma unroll
+        for (int f = 0; f < FM; ++f)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) mma(acc[f][j], bfr[ks][j], af[ks][f], EltBF16{});
+      if (h == kHalves - 1) {
+        if (last_kt) {
+          mfma_drain();
+          // DMA of K tile g + 1 has landed. Waited for before the stores below
+          // are issued: loads and stores on one counter may complete out of
+          // order. The stores drain during the next K tile, whose wait covers them.
+          if (grp == 0) wait_vm_lds<0>();
+          if (fp8) epilogue(g / nkt, std::true_type{});
+          else epilogue(g / nkt, std::false_type{});
+        } else if (grp == 0) {
+          wait_vm_lds<0>();   // DMA of K tile g + 1 has landed
+        }
+      }
+      lds_barrier();
+    }
+  }
+  if (grp == 0) lds_barrier();
+}
+
 // ---- k_outproj: out = mid U_out + bias  (model.py:101) --------------------
 // Both operands arrive by DMA through NS LDS stages.
 template <class Elt, int BM, int BN, int WM, int WN, int NS>
@@ -1292,6 +1506,31 @@ __global__ void k_transpose_e4m3(const uint8_t* __restrict__ src, uint16_t* __re
     const int64_t r = r0 + rr, c = c0 + cc;
     if (r < rows && c < cols) dst[c * rows + r] = t[rr][cc];
   }
+}
+
+// P^T of k_core_pp from core (r1, r3, r2): row (qb * r1 + r) * 32 + qq, column s
+// holds core[r, s, 32 qb + qq]. Source bf16 bits (codes == false) or e4m3 codes
+// with per-channel scales sc (r1, r2), a channel whose scale is zero packed as
+// zeros. One work-group per (channel block qb, 32 columns s, rank r).
+template <bool kE4M3>
+__global__ void k_pack_core_p(const void* __restrict__ src, uint16_t* __restrict__ dst,
+                              int64_t r1, int64_t r3, int64_t r2, const float* __restrict__ sc) {
+  __shared__ uint16_t t[32][33];
+  const int64_t qb = blockIdx.x, s0 = (int64_t)blockIdx.y * 32, r = blockIdx.z;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8 threads
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t i = (r * r3 + s0 + y) * r2 + qb * 32 + tx;
+    uint16_t v;
+    if constexpr (kE4M3) {
+      v = e4m3_to_bf16_bits(static_cast<const uint8_t*>(src)[i]);
+      if (sc && sc[r * r2 + qb * 32 + tx] == 0.f) v = 0;
+    } else {
+      v = static_cast<const uint16_t*>(src)[i];
+    }
+    t[y][tx] = v;
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) dst[((qb * r1 + r) * 32 + y) * r3 + s0 + tx] = t[tx][y];
 }
 
 // Core scale table of CoreRescale from sc (r1, r2): cs[r, q] = sc'[r, q] /

@@ -96,6 +96,7 @@ SHAPES = [
     (32, 3, 2, 64, 128, 128, 96),       # r3 = 64, E_pad 32
     (100, 5, 8, 128, 192, 320, 160),    # E_pad 128, odd k
     (64, 4, 1, 256, 64, 64, 64),        # r1 = 1, tiny r2
+    (16, 2, 1, 128, 512, 256, 128),     # r1 = 1 on the persistent core (r1 * r2 = 512)
     (8, 2, 32, 256, 512, 768, 4608),    # the reference's default ranks (config.py:20-24)
 ]
 
@@ -216,13 +217,15 @@ def test_fp8_full_size(pkg, dev):
     _check(w, got, ref64, "C5/full", tref)
 
 
+@pytest.mark.parametrize("r1,r2", [(3, 320), (4, 256)])
 @pytest.mark.parametrize("T", [40, 300])
-def test_fp8_every_code_and_zero_scales(pkg, dev, T):
+def test_fp8_every_code_and_zero_scales(pkg, dev, T, r1, r2):
     """Every finite e4m3 code appears in each weight, with some channels' scales
-    zero (and, for core, a zero scale between non-zero ones of the same column),
-    on a partial last core tile (r2 = 320) and r1 = 3; T = 40 takes the small-T
-    kernels, T = 300 the large-tile ones."""
-    w = pkg.Workload("fp8-codes", T, 256, 192, 8, 2, 3, 128, 320, torch.bfloat16, 91)
+    zero (and, for core, a zero scale between non-zero ones of the same column).
+    r1 = 3 with r2 = 320 runs the rank-rescaling core on a partial last tile,
+    r1 = 4 with r2 = 256 the persistent core (scales in its epilogue); T = 40 takes
+    the small-T kernels, T = 300 the large-tile ones."""
+    w = pkg.Workload("fp8-codes", T, 256, 192, 8, 2, r1, 128, r2, torch.bfloat16, 91)
     p32 = pkg.synth.make_params(w, affine="random", dtype=torch.float32)
     finite = torch.tensor([b for b in range(256) if b not in (0x7F, 0xFF)], dtype=torch.uint8)
     g = torch.Generator().manual_seed(5)
@@ -241,7 +244,7 @@ def test_fp8_every_code_and_zero_scales(pkg, dev, T):
     }
     codes["U_in_scale"][::7] = 0
     codes["core_scale"][1, ::5] = 0        # rank 1 of every 5th column: 0 between non-zero
-    codes["core_scale"][2, 3::11] = 0      # the last rank
+    codes["core_scale"][-1, 3::11] = 0     # the last rank
     codes["U_out_scale"][::13] = 0
     params = {k: v.to(torch.bfloat16) for k, v in p32.items()}
     ref = _fp8_reference(params, codes)
