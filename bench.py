@@ -226,7 +226,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         threads = torch.get_num_threads()
-        chunk = 512
+        chunk = min(512, T)   # tokens per CPU pass; the sample is whole chunks
         xs = x0[:chunk]
         t_a = time.perf_counter()
         # fp8: the reference runs on the dequantised weights, held in bf16 as the
