@@ -1203,6 +1203,9 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
   __shared__ u32x4 smem[TL::kLdsBytes / 16 + kScaleFloats / 4 + 3 * kCBuf / 4];
   float* sc_lds = reinterpret_cast<float*>(smem + TL::kLdsBytes / 16);
   float* c_lds = sc_lds + kScaleFloats;   // [3][BM][R1]
+  // without fp8 scales their region holds each wave's 2 KB transposition slot
+  static_assert(kScaleFloats * 4 >= 8 * 2048, "transposition slots");
+  char* slot = reinterpret_cast<char*>(sc_lds) + (threadIdx.x >> 6) * 2048;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
@@ -1273,43 +1276,62 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
     int tm, tn;
     coords(i, tm, tn);
     const int64_t m0 = (int64_t)tm * TL::BM;
-    float cf[FM][R1];
-#pragma unroll
-    for (int f = 0; f < FM; ++f)
-#pragma unroll
-      for (int r = 0; r < R1; ++r)
-        cf[f][r] = c_lds[(i % 3) * kCBuf + (wm * TL::kWaveM + 32 * f + (lane & 31)) * R1 + r];
 #pragma unroll
     for (int g = 0; g < QG; ++g) {
       // channel block of column blocks g * R1 .. g * R1 + R1 - 1 of this wave
       const int qb = tn * (TL::BN / 32 / R1) + (wn * FN) / R1 + g;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int q = qb * 32 + 8 * u + 4 * (lane >> 5);
-        float sv[R1][4];
+      for (int f = 0; f < FM; ++f) {
+        // one row block at a time (the scheduler would otherwise interleave the
+        // blocks and spill)
+        __builtin_amdgcn_sched_barrier(0);
+        float cf[R1];
 #pragma unroll
         for (int r = 0; r < R1; ++r)
+          cf[r] = c_lds[(i % 3) * kCBuf + (wm * TL::kWaveM + 32 * f + (lane & 31)) * R1 + r];
+        const int64_t row = m0 + wm * TL::kWaveM + 32 * f + (lane & 31);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) sv[r][v] = kFp8 ? sc_lds[r * r2 + q + v] : 1.f;
-#pragma unroll
-        for (int f = 0; f < FM; ++f) {
-          const int64_t row = m0 + wm * TL::kWaveM + 32 * f + (lane & 31);
+        for (int u = 0; u < 4; ++u) {
+          const int q = qb * 32 + 8 * u + 4 * (lane >> 5);
           float o[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             float sum = 0.f;
 #pragma unroll
             for (int r = 0; r < R1; ++r) {
-              const float y = kFp8 ? acc[f][g * R1 + r][4 * u + v] * sv[r][v]
+              const float y = kFp8 ? acc[f][g * R1 + r][4 * u + v] * sc_lds[r * r2 + q + v]
                                    : acc[f][g * R1 + r][4 * u + v];
-              sum += cf[f][r] * y;
+              sum += cf[r] * y;
             }
             o[v] = sum;
           }
           uint2 pk;
           pk.x = pack_bf16x2(o[0], o[1]);
           pk.y = pack_bf16x2(o[2], o[3]);
-          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.mid) + row * r2 + q) = pk;
+          if constexpr (kFp8) {
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.mid) + row * r2 + q) = pk;
+          } else {
+            // into this wave's slot: row lane & 31, 16-byte chunk u (swizzled by
+            // row >> 2), half lane >> 5
+            const int r = lane & 31;
+            *reinterpret_cast<uint2*>(slot + r * 64 + 16 * (u ^ ((r >> 2) & 3)) +
+                                      8 * (lane >> 5)) = pk;
+          }
+        }
+        if constexpr (!kFp8) {
+          // the block's 32 rows x 32 channels leave as row-contiguous 64-byte pieces,
+          // 16 rows a store instead of 32 rows of 16 bytes (LDS operations of one
+          // wave complete in order: the reads see the writes above, and the next
+          // block's writes follow these reads)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int rr = 16 * hh + (lane >> 2), ch = lane & 3;
+            const u32x4 v =
+                *reinterpret_cast<const u32x4*>(slot + rr * 64 + 16 * (ch ^ ((rr >> 2) & 3)));
+            const int64_t orow = m0 + wm * TL::kWaveM + 32 * f + rr;
+            *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.mid) + orow * r2 + qb * 32 +
+                                      8 * ch) = v;
+          }
         }
       }
     }
