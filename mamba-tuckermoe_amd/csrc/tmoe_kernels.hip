@@ -26,11 +26,18 @@ struct CoreCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P =
 struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 2; };
 
 // Front tiles: kFrontBM tokens in kFrontWM row groups; with the widest router
-// (E > 128) one group of 32 tokens, whose smaller LDS footprint measured faster.
+// (E > 128) one group of 32 tokens, whose smaller LDS footprint measured faster,
+// or, with r3 = 256, separate z and router work-groups of 32 tokens.
 // The weight rows come from L2 one DMA per K tile; a third LDS stage (when it
 // fits) issues them two tiles ahead, which hides the L2 latency.
 template <class Elt, int R3, int NR>
 hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
+  if constexpr (R3 == 256 && NR == 8 && std::is_same<Elt, EltBF16>::value) {
+    // z and router work-groups of 32 tokens (k_front_split), three LDS stages
+    const dim3 grid(2 * cdiv(a.T, 32)), block(256);
+    hipLaunchKernelGGL((dev::k_front_split<Elt, R3, NR, kFrontPFA, 3>), grid, block, 0, st, a);
+    return hipGetLastError();
+  }
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
   constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
   constexpr int kStageBytes = (BM + R3 + 32 * NR) * 128;

@@ -849,60 +849,20 @@ struct RouterExtra {
   __device__ __forceinline__ void tile_begin(int, ACC&) const {}
 };
 
-template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
-          int WMF = kFrontWM>
-__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
+// z = RMSNorm(x U_in) * g for the BM rows of a front tile (model.py:80-81, :25-27):
+// fp8 column scales, the row sums of squares (lane shuffles, then the waves'
+// partial sums in wave order by one thread per row), z / rms as z * (1 / rms)
+// (within one fp32 rounding of the division), staged in LDS at zst and written as
+// 16-byte chunks. red: LDS for [NW][BM] partial sums followed by [BM] 1 / rms.
+// Called by every thread of the work-group.
+template <class TL, class Elt, int R3>
+__device__ __forceinline__ void front_z_epilogue(f32x16 (&acc)[TL::FM][TL::FN], const FwdArgs& a,
+                                                 int64_t m0, int rows_valid, char* zst,
+                                                 float* red) {
   typedef typename Elt::T T;
-  constexpr int EP = 32 * NR;
-  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;   // waves across the z columns
-  constexpr int NWT = NW * WMF;                      // all waves (WMF row groups)
-  // x streams from HBM once: a register ring of PFA K tiles, run by half of the
-  // waves. The weight rows come from L2 by DMA into LDS (the other half), shared
-  // by the WMF row groups.
-  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
-  constexpr int FM = TL::FM;   // a wave covers the BM / WMF rows of its group
-  typedef RouterExtra<Elt, FM, NR, NW> RX;
-  // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
-  constexpr int LD = EP + 1;
-  constexpr int kPlanes = RX::kSplitK ? NW : 1;
-  constexpr int kZBytes = TileStage<TL, T>::kBytes;
-  // + per-row top-k record: exp weights, indices and final weights of the k
-  // rounds, the sum over the selected and the sum over all E
-  constexpr int kEpiBytes =
-      kZBytes + (kPlanes * BM * LD + NW * BM + BM + BM * (3 * kMaxTopK + 2)) * 4;
-  // U_expert is staged after that: at least 4 KB (E = 256, r1 = 4) of room
-  constexpr int kSmemBytes = cmax(TL::kLdsBytes, kEpiBytes + 4096);
-  __shared__ u32x4 smem[kSmemBytes / 16];
-
+  constexpr int FM = TL::FM, NW = TL::WN, BM = TL::BM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;   // column wave, first row
-  const int64_t m0 = (int64_t)blockIdx.x * BM;
-  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
-  const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
-  RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes, row_bytes, rows_valid};
-  RowLoader bl{reinterpret_cast<const char*>(a.wfront), row_bytes, R3 + EP};
-  f32x16 acc[FM][TL::FN];
-  RX rx;
-  rx.init(wn, lane, BM + R3);
-  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, rx);
-
-  // -- router logits -> LDS, [BM][EP + 1] (split-K: one partial plane per wave) --
-  char* zst = reinterpret_cast<char*>(smem);
-  float* lg = reinterpret_cast<float*>(zst + kZBytes);
-  float* red = lg + kPlanes * BM * LD;   // [NW][BM] RMSNorm partial sums
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < RX::RT; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = wrow + i * 32 + acc_row(lane, e);
-        if constexpr (RX::kSplitK)
-          lg[(wn * BM + row) * LD + j * 32 + (lane & 31)] = rx.racc[i][j][e];
-        else
-          lg[row * LD + (wn * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
-      }
-
+  const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;
   // -- fp8 weights: z column j = (x . q_in[:, j]) * s_in[j] ----------------
   if (a.zscale) {
 #pragma unroll
@@ -941,7 +901,6 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
     float tot = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) tot += red[w * BM + threadIdx.x];
-    // z / rms as z * (1 / rms): within one fp32 rounding of the division
     inv[threadIdx.x] = 1.f / sqrtf(tot / (float)R3 + a.eps);
   }
   __syncthreads();
@@ -968,32 +927,45 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   }
   __syncthreads();
   flush_tile<TL, T>(zst, reinterpret_cast<T*>(a.z) + m0 * R3, R3, rows_valid, R3);
+}
 
-  // -- top-k, softmax, c -------------------------------------------------------
-  // A row is resolved by a group of G lanes (1 to 8; as many as fill the
-  // work-group, and at least EP / 32) holding EP / G <= 32 logits each (columns
-  // gl, gl + G, ...): K rounds of a serial arg-max over the lane's logits and a
-  // DPP arg-max over the group, with no LDS traffic in the rounds. Round kk's
-  // exp(v - v_max) and index go to LDS; then the softmax weights and c are
-  // formed in parallel over (row, round) and (row, r). U_expert is read from
-  // LDS when it fits in the space left after the logits.
-  constexpr int kFill = 64 * NWT / BM;
+// LDS floats of front_topk's per-row record: exp weights, indices and final
+// weights of the k rounds, the sum over the selected and the sum over all E.
+template <int BM>
+constexpr int kTopkRecFloats = BM * (3 * kMaxTopK + 2);
+
+// Top-k, softmax and c for the BM rows of a front tile whose logits are in LDS
+// (model.py:76-77, :93): NP planes of [BM][LD] floats, a logit being the sum of
+// its planes in plane order. rec: kTopkRecFloats<BM> floats of LDS followed by
+// ue_bytes for U_expert. Called by every one of the NT threads of the work-group.
+// A row is resolved by a group of G lanes (1 to 8; as many as fill the
+// work-group, and at least EP / 32) holding EP / G <= 32 logits each (columns
+// gl, gl + G, ...): K rounds of a serial arg-max over the lane's logits and a
+// DPP arg-max over the group, with no LDS traffic in the rounds. Round kk's
+// exp(v - v_max) and index go to LDS; then the softmax weights and c are
+// formed in parallel over (row, round) and (row, r). U_expert is read from
+// LDS when it fits in ue_bytes.
+template <int EP, int BM, int NT, int NP>
+__device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int rows_valid,
+                                           const float* lg, int LD, float* rec, int ue_bytes) {
+  constexpr int NWT = NT / 64;
+  constexpr int kFill = NT / BM;
   constexpr int G = cmin(8, cmax(EP / 32, kFill < 1 ? 1 : kFill));
   constexpr int PL = EP / G;          // logits per lane
   static_assert(PL <= 32 && EP % G == 0, "taken-mask width");
   constexpr int RPW = 64 / G;         // rows per wave per pass
-  constexpr int kUeBytes = kSmemBytes - kEpiBytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
-  float* rec_ex = inv + BM;                       // [BM][kMaxTopK]
-  int* rec_i = reinterpret_cast<int*>(rec_ex + BM * kMaxTopK);   // [BM][kMaxTopK]
+  float* rec_ex = rec;                                              // [BM][kMaxTopK]
+  int* rec_i = reinterpret_cast<int*>(rec_ex + BM * kMaxTopK);      // [BM][kMaxTopK]
   float* rec_w = reinterpret_cast<float*>(rec_i + BM * kMaxTopK);   // [BM][kMaxTopK]
   float* rec_sum = rec_w + BM * kMaxTopK;         // [BM] over the selected
   float* rec_all = rec_sum + BM;                  // [BM] over all E (router_mode 1)
   float* ue = rec_all + BM;
   const int mode = a.router_mode;
-  const bool ue_lds = E * R1 * 4 <= kUeBytes;
+  const bool ue_lds = E * R1 * 4 <= ue_bytes;
   if (ue_lds)
-    for (int i = threadIdx.x; i < E * R1; i += TL::kThreads) ue[i] = a.uexp[i];
+    for (int i = threadIdx.x; i < E * R1; i += NT) ue[i] = a.uexp[i];
   const float* uex = ue_lds ? ue : a.uexp;
   const int gl = lane % G;
   for (int row0 = wave * RPW; row0 < BM; row0 += NWT * RPW) {
@@ -1008,12 +980,8 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
     for (int p = 0; p < PL; ++p) {
       const int col = gl + G * p;
       float sc = 0.f;
-      if constexpr (RX::kSplitK) {
 #pragma unroll
-        for (int w = 0; w < NW; ++w) sc += lg[(w * BM + row) * LD + col];
-      } else {
-        sc = lg[row * LD + col];
-      }
+      for (int w = 0; w < NP; ++w) sc += lg[(w * BM + row) * LD + col];
       if (a.logits && live && col < E) a.logits[g * E + col] = sc;
       sv[p] = mode ? capped_score(sc, a.router_scale, a.router_temperature) : sc;
       key[p] = col < E ? rank_key(sv[p], col) : 0;
@@ -1049,7 +1017,7 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   }
   __syncthreads();
   // routing weights (model.py:77) and c = sum_j w_j U_expert[e_j] (model.py:93)
-  for (int q = threadIdx.x; q < rows_valid * K; q += TL::kThreads) {
+  for (int q = threadIdx.x; q < rows_valid * K; q += NT) {
     const int row = q / K, kk = q - row * K;
     const float wk = slot_weight(mode, rec_ex + row * kMaxTopK, K, kk, rec_sum[row],
                                  mode ? rec_all[row] : 0.f);
@@ -1058,12 +1026,125 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
     rec_w[row * kMaxTopK + kk] = wk;
   }
   __syncthreads();
-  for (int q = threadIdx.x; q < rows_valid * R1; q += TL::kThreads) {
+  for (int q = threadIdx.x; q < rows_valid * R1; q += NT) {
     const int row = q / R1, r = q - row * R1;
     float cr = 0.f;
     for (int kk = 0; kk < K; ++kk)
       cr += rec_w[row * kMaxTopK + kk] * uex[rec_i[row * kMaxTopK + kk] * R1 + r];
     a.c[(m0 + row) * R1 + r] = cr;
+  }
+}
+
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
+          int WMF = kFrontWM>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
+  typedef typename Elt::T T;
+  constexpr int EP = 32 * NR;
+  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;   // waves across the z columns
+  constexpr int NWT = NW * WMF;                      // all waves (WMF row groups)
+  // x streams from HBM once: a register ring of PFA K tiles, run by half of the
+  // waves. The weight rows come from L2 by DMA into LDS (the other half), shared
+  // by the WMF row groups.
+  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
+  constexpr int FM = TL::FM;   // a wave covers the BM / WMF rows of its group
+  typedef RouterExtra<Elt, FM, NR, NW> RX;
+  // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
+  // and 1 / rms, then the top-k record
+  constexpr int LD = EP + 1;
+  constexpr int kPlanes = RX::kSplitK ? NW : 1;
+  constexpr int kZBytes = TileStage<TL, T>::kBytes;
+  constexpr int kEpiBytes = kZBytes + (kPlanes * BM * LD + NW * BM + BM + kTopkRecFloats<BM>) * 4;
+  // U_expert is staged after that: at least 4 KB (E = 256, r1 = 4) of room
+  constexpr int kSmemBytes = cmax(TL::kLdsBytes, kEpiBytes + 4096);
+  __shared__ u32x4 smem[kSmemBytes / 16];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;   // column wave, first row
+  const int64_t m0 = (int64_t)blockIdx.x * BM;
+  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+  const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
+  RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes, row_bytes, rows_valid};
+  RowLoader bl{reinterpret_cast<const char*>(a.wfront), row_bytes, R3 + EP};
+  f32x16 acc[FM][TL::FN];
+  RX rx;
+  rx.init(wn, lane, BM + R3);
+  gemm_mainloop<TL, Elt>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem, rx);
+
+  // -- router logits -> LDS, [BM][EP + 1] (split-K: one partial plane per wave) --
+  char* zst = reinterpret_cast<char*>(smem);
+  float* lg = reinterpret_cast<float*>(zst + kZBytes);
+  float* red = lg + kPlanes * BM * LD;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < RX::RT; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wrow + i * 32 + acc_row(lane, e);
+        if constexpr (RX::kSplitK)
+          lg[(wn * BM + row) * LD + j * 32 + (lane & 31)] = rx.racc[i][j][e];
+        else
+          lg[row * LD + (wn * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
+      }
+  front_z_epilogue<TL, Elt, R3>(acc, a, m0, rows_valid, zst, red);
+  front_topk<EP, BM, TL::kThreads, kPlanes>(a, m0, rows_valid, lg, LD, red + NW * BM + BM,
+                                            kSmemBytes - kEpiBytes);
+}
+
+// The front for wide routers (E_pad = 32 NR > 128 with r3 = R3 = 256), in two kinds
+// of work-group over 32-token tiles: the first ceil(T / 32) compute z (x against
+// U_in^T, RMSNorm), the others the logits (x against the router rows, top-k,
+// softmax, c). The two halves are independent, and splitting them doubles the
+// work-groups (128 of the single kind at T = 4096 left half of 256 CUs idle) and
+// halves the weight rows each streams. 4 waves each, wave tile 32 x (columns / 4).
+template <class Elt, int R3, int NR, int PFA, int NS>
+__global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
+  typedef typename Elt::T T;
+  constexpr int BM = 32, EP = 32 * NR, NW = 4;
+  static_assert(R3 == 256 && EP >= 128, "split front: r3 = 256, E_pad >= 128");
+  typedef Tile<BM, R3, 0, 1, NW, PFA, 1, NS, false, true, NW / 2> TLZ;
+  typedef Tile<BM, EP, 0, 1, NW, PFA, 1, NS, false, true, NW / 2> TLR;
+  constexpr int LD = EP + 1;
+  constexpr int kZEpi = TileStage<TLZ, T>::kBytes + (NW * BM + BM) * 4;
+  constexpr int kREpi = (BM * LD + kTopkRecFloats<BM>) * 4;
+  constexpr int kUe = 4096;   // U_expert (E = 256, r1 = 4) when it fits
+  constexpr int kSmemBytes =
+      cmax(cmax(TLZ::kLdsBytes, TLR::kLdsBytes), cmax(kZEpi, kREpi + kUe));
+  __shared__ u32x4 smem[kSmemBytes / 16];
+
+  const int ntm = (int)((a.T + BM - 1) / BM);
+  const bool zpart = (int)blockIdx.x < ntm;   // uniform over the work-group
+  const int tm = zpart ? (int)blockIdx.x : (int)blockIdx.x - ntm;
+  const int64_t m0 = (int64_t)tm * BM;
+  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+  const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
+  const int nkt = (int)(row_bytes / kTileKBytes);
+  RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes, row_bytes, rows_valid};
+  NoExtra nx;
+  if (zpart) {
+    RowLoader bl{reinterpret_cast<const char*>(a.wfront), row_bytes, R3};
+    f32x16 acc[TLZ::FM][TLZ::FN];
+    gemm_mainloop<TLZ, Elt>(acc, al, bl, nkt, smem, nx);
+    char* zst = reinterpret_cast<char*>(smem);
+    front_z_epilogue<TLZ, Elt, R3>(acc, a, m0, rows_valid, zst,
+                                   reinterpret_cast<float*>(zst + TileStage<TLZ, T>::kBytes));
+  } else {
+    RowLoader bl{reinterpret_cast<const char*>(a.wfront) + R3 * row_bytes, row_bytes, EP};
+    f32x16 acc[TLR::FM][TLR::FN];
+    gemm_mainloop<TLR, Elt>(acc, al, bl, nkt, smem, nx);
+    const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) % NW;
+    float* lg = reinterpret_cast<float*>(smem);   // [BM][LD]
+#pragma unroll
+    for (int i = 0; i < TLR::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < TLR::FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          lg[(i * 32 + acc_row(lane, e)) * LD + wn * TLR::kWaveN + j * 32 + (lane & 31)] =
+              acc[i][j][e];
+    __syncthreads();
+    front_topk<EP, BM, TLR::kThreads, 1>(a, m0, rows_valid, lg, LD, lg + BM * LD,
+                                         kSmemBytes - kREpi);
   }
 }
 
