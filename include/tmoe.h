@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 2
+#define TMOE_ABI_VERSION 3
 
 /* error codes */
 #define TMOE_OK            0
@@ -144,6 +144,40 @@ int tmoe_pack_weights_fp8(const tmoe_plan* plan, const void* router_w,
 int tmoe_forward(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
                  void* out, int32_t* topk_idx, float* topk_w, float* logits,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused elementwise epilogues of tmoe_forward_epi (the FFN sub-block of the
+ * reference's TransformerBlock, model.py:337-341). y is the layer output
+ * TuckerMoE.forward(x) rounded to the plan dtype; R() rounds to the plan dtype.
+ *   TMOE_EPI_NONE            out = y
+ *   TMOE_EPI_GLU             out = R(R(silu(epi_a)) * y)        F.silu(gate) * up   (:340)
+ *                            epi_a = gate (T, d_out), silu(g) = g / (1 + exp(-g))
+ *   TMOE_EPI_RESIDUAL_SCALE  out = R(epi_a + R(epi_b * y))       x_res + ls_ffn(dn)  (:341)
+ *                            epi_a = x_res (T, d_out), epi_b = LayerScale gamma (d_out)
+ *                            (LayerScale.forward, model.py:35-36) */
+#define TMOE_EPI_NONE           0
+#define TMOE_EPI_GLU            1
+#define TMOE_EPI_RESIDUAL_SCALE 2
+
+/* tmoe_forward with one of the TMOE_EPI_* ops fused into the out-projection's
+ * store: no counterpart of its own in the reference, it computes the expression
+ * of model.py:340 or :341 that consumes this layer's output (ffn_up's output with
+ * epi = GLU of the gate output; ffn_down's with epi = RESIDUAL_SCALE). epi_a and
+ * epi_b are device tensors in the plan's activation dtype (bf16 for
+ * TMOE_BF16_FP8W), 16-byte aligned; epi_a may be `out` itself (each element is
+ * read before it is written, by the same thread), which updates a residual
+ * stream in place. Other arguments and errors as tmoe_forward; tmoe_forward is
+ * tmoe_forward_epi with TMOE_EPI_NONE. */
+int tmoe_forward_epi(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
+                     void* out, int32_t* topk_idx, float* topk_w, float* logits,
+                     void* workspace, size_t workspace_bytes, int epi_mode,
+                     const void* epi_a, const void* epi_b, void* stream);
+
+/* out (T, d) = RMSNorm(x) (T, d) with gain weight (d): RMSNorm.forward of
+ * model.py:25-27, (x / sqrt(mean(x^2) + eps)) * weight, computed in fp32 and
+ * rounded to dtype (TMOE_BF16 or TMOE_F32) once. The FFN sub-block's norm_ffn
+ * (model.py:337). out may not overlap x. Stream-ordered, no allocation. */
+int tmoe_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* weight, float eps,
+                      int dtype, void* out, void* stream);
 
 /* Per-stage timing, no counterpart in the reference (measurement support).
  * While enabled, every tmoe_forward records a HIP event before each of its

@@ -5,14 +5,20 @@ Public surface:
   TuckerMoE(d_in, d_out, cfg)  drop-in nn.Module (module.py)
   TuckerMoEConfig              the cfg fields the module reads (config.py)
   WORKLOADS                    the named seeded workloads C1..C5 (config.py)
+  FFN_WORKLOADS                seeded FFN sub-block configurations F0..F2 (config.py)
   load_tucker                  checkpoint-key loader that refreshes packed weights
+  TuckerFFN, TuckerOutProj     the reference blocks' Tucker-MoE sub-blocks (block.py):
+                               TransformerBlock's FFN, Mamba3Block's out_proj
+  RMSNorm, LayerScale          their norm and scale modules
   synth                        seeded synthetic parameters and tokens
   fp8                          e4m3 weights with per-output-channel scales
   _lib                         ctypes binding of the C ABI (include/tmoe.h)
 """
 from . import _lib, config, fp8, synth
-from .config import WORKLOADS, TuckerMoEConfig, Workload
+from .config import FFN_WORKLOADS, WORKLOADS, FfnWorkload, TuckerMoEConfig, Workload
 from .module import RMSNorm, TuckerMoE, load_tucker
+from .block import LayerScale, TuckerFFN, TuckerOutProj
 
-__all__ = ["TuckerMoE", "RMSNorm", "TuckerMoEConfig", "Workload", "WORKLOADS", "load_tucker",
-           "synth", "config", "fp8", "_lib"]
+__all__ = ["TuckerMoE", "RMSNorm", "LayerScale", "TuckerFFN", "TuckerOutProj",
+           "TuckerMoEConfig", "Workload", "WORKLOADS", "FfnWorkload", "FFN_WORKLOADS", "load_tucker", "synth", "config", "fp8",
+           "_lib"]

@@ -19,10 +19,11 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
+TMOE_EPI_NONE, TMOE_EPI_GLU, TMOE_EPI_RESIDUAL_SCALE = 0, 1, 2
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
 
@@ -30,7 +31,7 @@ STAGE_NAMES = ("front", "core", "out_proj")
 EXPORTED = (
     "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
     "tmoe_packed_bytes", "tmoe_workspace_bytes", "tmoe_pack_weights", "tmoe_pack_weights_fp8",
-    "tmoe_forward",
+    "tmoe_forward", "tmoe_forward_epi", "tmoe_rmsnorm_rows",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
 
@@ -92,6 +93,11 @@ def lib() -> ctypes.CDLL:
         L.tmoe_pack_weights_fp8.argtypes = [vp] * 13
         L.tmoe_forward.restype = ctypes.c_int
         L.tmoe_forward.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]
+        L.tmoe_forward_epi.restype = ctypes.c_int
+        L.tmoe_forward_epi.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, ctypes.c_int,
+                                       vp, vp, vp]
+        L.tmoe_rmsnorm_rows.restype = ctypes.c_int
+        L.tmoe_rmsnorm_rows.argtypes = [vp, i64, i64, vp, ctypes.c_float, ctypes.c_int, vp, vp]
         L.tmoe_prof_enable.restype = ctypes.c_int
         L.tmoe_prof_enable.argtypes = [ctypes.c_int]
         L.tmoe_prof_read.restype = ctypes.c_int
@@ -109,6 +115,15 @@ def check(rc: int) -> int:
     if rc < 0:
         raise TmoeError(rc, lib().tmoe_last_error().decode(errors="replace"))
     return rc
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    """TMOE_BF16 / TMOE_F32 for an activation dtype; raises for any other."""
+    if dtype == torch.bfloat16:
+        return TMOE_BF16
+    if dtype == torch.float32:
+        return TMOE_F32
+    raise TmoeError(TMOE_EUNSUPPORTED, f"dtype {dtype}: supported are bfloat16 and float32")
 
 
 class Plan:

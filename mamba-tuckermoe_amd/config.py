@@ -21,6 +21,7 @@ class TuckerMoEConfig:
     kmoe_r1: int = 32                 # config.py:22
     kmoe_r2: int = 512                # config.py:23
     kmoe_r3: int = 256                # config.py:24
+    ffn_expand: int = 6               # config.py:17 (TuckerFFN: d_ff = ffn_expand * d)
 
 
 @dataclass(frozen=True)
@@ -109,4 +110,52 @@ WORKLOADS = {
                    router_std=0.02, note="expert-count scaling"),
     "C5": Workload("C5", 16384, 1536, 2304, 16, 2, 4, 256, 1024, torch.bfloat16, 1005,
                    fp8=True, note="fp8 e4m3 U_in/core/U_out with per-output-channel scales"),
+}
+
+
+@dataclass(frozen=True)
+class FfnWorkload:
+    """One seeded synthetic configuration of TransformerBlock's FFN sub-block
+    (model.py:292-296): ffn_gate / ffn_up TuckerMoE(d, d_ff), ffn_down
+    TuckerMoE(d_ff, d), d_ff = ffn_expand * d."""
+    name: str
+    T: int
+    d: int
+    ffn_expand: int
+    E: int
+    k: int
+    r1: int
+    r3: int
+    r2: int
+    dtype: torch.dtype
+    seed: int
+    note: str = ""
+
+    @property
+    def d_ff(self) -> int:
+        return self.ffn_expand * self.d
+
+    def cfg(self, eps: float = 1e-5) -> TuckerMoEConfig:
+        return TuckerMoEConfig(rms_norm_eps=eps, kmoe_num_experts=self.E, kmoe_top_k=self.k,
+                               kmoe_r1=self.r1, kmoe_r2=self.r2, kmoe_r3=self.r3,
+                               ffn_expand=self.ffn_expand)
+
+    def layer(self, name: str) -> Workload:
+        """The Workload of sub-layer ffn_gate / ffn_up / ffn_down (its own seed)."""
+        i = ("ffn_gate", "ffn_up", "ffn_down").index(name)
+        d_in, d_out = (self.d, self.d_ff) if i < 2 else (self.d_ff, self.d)
+        return Workload(f"{self.name}.{name}", self.T, d_in, d_out, self.E, self.k, self.r1,
+                        self.r3, self.r2, self.dtype, self.seed * 8 + 1 + i)
+
+
+FFN_WORKLOADS = {
+    # the reference checkpoint's block (config.py: d_model 768, ffn_expand 6, E 8,
+    # k 2, r = (32, 512, 256)); r1 = 32 takes the row-blocked core
+    "F1": FfnWorkload("F1", 4096, 768, 6, 8, 2, 32, 256, 512, torch.bfloat16, 2001,
+                      note="TransformerBlock FFN at the reference model's dimensions"),
+    # the same shape with r1 = 4, on the persistent core
+    "F2": FfnWorkload("F2", 4096, 768, 6, 8, 2, 4, 256, 512, torch.bfloat16, 2002,
+                      note="FFN with rank r1 = 4"),
+    "F0": FfnWorkload("F0", 64, 256, 2, 8, 2, 4, 128, 256, torch.float32, 2000,
+                      note="small fp32 FFN for CPU oracle checks"),
 }

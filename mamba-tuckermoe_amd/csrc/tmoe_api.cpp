@@ -304,8 +304,22 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
 int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
                  int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
                  size_t workspace_bytes, void* stream) {
+  return tmoe_forward_epi(p, x, T, packed, out, topk_idx, topk_w, logits, workspace,
+                          workspace_bytes, TMOE_EPI_NONE, nullptr, nullptr, stream);
+}
+
+int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
+                     int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
+                     size_t workspace_bytes, int epi_mode, const void* epi_a, const void* epi_b,
+                     void* stream) {
   g_err[0] = 0;
   if (!p) return fail(TMOE_EINVAL, "tmoe_forward: null plan");
+  if (epi_mode != TMOE_EPI_NONE && epi_mode != TMOE_EPI_GLU && epi_mode != TMOE_EPI_RESIDUAL_SCALE)
+    return fail(TMOE_EINVAL, "tmoe_forward_epi: epi_mode %d is not a TMOE_EPI_* value", epi_mode);
+  if (epi_mode != TMOE_EPI_NONE && (!epi_a || !aligned16(epi_a)))
+    return fail(TMOE_EINVAL, "tmoe_forward_epi: epi_a must be a 16-byte aligned (T, d_out) tensor");
+  if (epi_mode == TMOE_EPI_RESIDUAL_SCALE && (!epi_b || !aligned16(epi_b)))
+    return fail(TMOE_EINVAL, "tmoe_forward_epi: epi_b (gamma) must be 16-byte aligned");
   if (T < 0) return fail(TMOE_EINVAL, "tmoe_forward: T=%lld < 0", (long long)T);
   if (T > (int64_t)1 << 30) return fail(TMOE_EUNSUPPORTED, "tmoe_forward: T=%lld too large",
                                         (long long)T);
@@ -351,6 +365,9 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.z = ws + L.z;
   a.mid = ws + L.mid;
   a.raw = reinterpret_cast<float*>(ws + L.raw);
+  a.epi_mode = epi_mode;
+  a.epi_a = epi_mode != TMOE_EPI_NONE ? epi_a : nullptr;
+  a.epi_b = epi_mode == TMOE_EPI_RESIDUAL_SCALE ? epi_b : nullptr;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
@@ -382,6 +399,21 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
     g_prof.pending.push_back(std::move(ev));
   }
   return TMOE_OK;
+}
+
+int tmoe_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* weight, float eps,
+                      int dtype, void* out, void* stream) {
+  g_err[0] = 0;
+  if (dtype != TMOE_BF16 && dtype != TMOE_F32)
+    return fail(TMOE_EINVAL, "tmoe_rmsnorm_rows: dtype %d is not TMOE_BF16 or TMOE_F32", dtype);
+  if (T < 0 || d <= 0)
+    return fail(TMOE_EINVAL, "tmoe_rmsnorm_rows: T=%lld, d=%lld", (long long)T, (long long)d);
+  if (!(eps >= 0.f)) return fail(TMOE_EINVAL, "tmoe_rmsnorm_rows: eps must be >= 0");
+  if (T == 0) return TMOE_OK;
+  if (!x || !weight || !out) return fail(TMOE_EINVAL, "tmoe_rmsnorm_rows: null x/weight/out");
+  const hipError_t e = tmoe::launch_rmsnorm_rows(x, T, d, weight, eps, dtype, out,
+                                                 static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_rmsnorm_rows");
 }
 
 int tmoe_prof_enable(int on) {

@@ -50,7 +50,15 @@ struct FwdArgs {
   void* z;                      // (T, r3)
   void* mid;                    // (T, r2)
   float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
+  // elementwise op fused into the out-projection's store (kEpi*): the FFN
+  // sub-block's silu(gate) * up, or its residual + LayerScale
+  int epi_mode;
+  const void* epi_a;            // (T, d_out) dtype     gate output / residual input
+  const void* epi_b;            // (d_out) dtype        LayerScale gamma
 };
+
+// fused out-projection epilogues (TMOE_EPI_* of include/tmoe.h)
+constexpr int kEpiNone = 0, kEpiGlu = 1, kEpiResScale = 2;
 
 // Token counts up to kSmallT take the small-T path (tmoe_small.hpp).
 constexpr int64_t kSmallT = 256;
@@ -95,5 +103,8 @@ hipError_t launch_copy_pad(const void* src, void* dst, int64_t n, int64_t n_pad,
                            hipStream_t stream);
 // dst[i] = float(src[i]) for n elements of dtype (TMOE_BF16 / TMOE_F32).
 hipError_t launch_to_f32(const void* src, float* dst, int64_t n, int dtype, hipStream_t stream);
+// out (T, d) = RMSNorm of each row of x (T, d) with gain w (d), dtype TMOE_BF16 / TMOE_F32.
+hipError_t launch_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* w, float eps,
+                               int dtype, void* out, hipStream_t stream);
 
 }  // namespace tmoe

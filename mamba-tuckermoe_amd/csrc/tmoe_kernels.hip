@@ -250,6 +250,20 @@ hipError_t launch_copy_pad(const void* src, void* dst, int64_t n, int64_t n_pad,
   return hipGetLastError();
 }
 
+hipError_t launch_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* w, float eps,
+                               int dtype, void* out, hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid(cdiv(T, 4)), block(256);
+  if (dtype == kDtypeBF16)
+    hipLaunchKernelGGL(dev::k_rmsnorm_rows<uint16_t>, grid, block, 0, st,
+                       static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w), eps,
+                       static_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(dev::k_rmsnorm_rows<float>, grid, block, 0, st, static_cast<const float*>(x),
+                       T, d, static_cast<const float*>(w), eps, static_cast<float*>(out));
+  return hipGetLastError();
+}
+
 hipError_t launch_to_f32(const void* src, float* dst, int64_t n, int dtype, hipStream_t st) {
   if (n == 0) return hipSuccess;
   const dim3 grid(cdiv(n, 256) < 4096 ? cdiv(n, 256) : 4096), block(256);

@@ -695,19 +695,68 @@ __device__ __forceinline__ void stage_tile_t(const f32x16 (&acc)[TL::FM][TL::FN]
     }
 }
 
-// flush_tile by the NT threads t0 .. t0 + NT - 1 of the work-group (tid: this
-// thread's index among them).
+// ---- fused FFN epilogues of the out-projection -----------------------------
+// The FFN sub-block of the reference's TransformerBlock (model.py:337-341) passes
+// an out-projection's output y (the layer output, already rounded to the module
+// dtype) through one elementwise op, which is fused into its store:
+//   kEpiGlu       out = R(R(silu(g)) * y), g = epi_a[row, col]     F.silu(gate) * up
+//   kEpiResScale  out = R(x + R(gamma[col] * y)), x = epi_a[row, col], gamma = epi_b
+//                                                    x_res + ls_ffn(dn)   (:35-36, :341)
+// R rounds to the module dtype, as each of the reference module's ops does;
+// silu(g) = g / (1 + exp(-g)) in fp32.
+__device__ __forceinline__ float round_as(float v, EltBF16) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+__device__ __forceinline__ float round_as(float v, EltF32) { return v; }
+template <class Elt>
+__device__ __forceinline__ float epi_value(int mode, float y, float ea, float eb) {
+#pragma clang fp contract(off)   // x + gamma * y is two rounded ops, as in the reference
+  if (mode == kEpiGlu) return round_as(round_as(ea / (1.f + expf(-ea)), Elt{}) * y, Elt{});
+  return round_as(ea + round_as(eb * y, Elt{}), Elt{});
+}
+// epi_value over one 16-byte chunk y of output row `row`, columns col .. col + 16 /
+// sizeof(T) - 1 (chunks never straddle the valid columns)
+template <class T>
+__device__ __forceinline__ u32x4 epi_chunk(const FwdArgs& a, u32x4 y, int64_t row, int64_t col) {
+  const u32x4 ea =
+      *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.epi_a) + row * a.d_out + col);
+  const u32x4 eb = a.epi_mode == kEpiResScale
+                       ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.epi_b) + col)
+                       : u32x4{0u, 0u, 0u, 0u};
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (sizeof(T) == 2) {
+      const float lo = epi_value<EltBF16>(a.epi_mode, bf16_bits_to_f32(y[j] & 0xffffu),
+                                          bf16_bits_to_f32(ea[j] & 0xffffu),
+                                          bf16_bits_to_f32(eb[j] & 0xffffu));
+      const float hi = epi_value<EltBF16>(a.epi_mode, bf16_bits_to_f32(y[j] >> 16),
+                                          bf16_bits_to_f32(ea[j] >> 16),
+                                          bf16_bits_to_f32(eb[j] >> 16));
+      o[j] = pack_bf16x2(lo, hi);   // exact: both are bf16 values
+    } else {
+      o[j] = __float_as_uint(epi_value<EltF32>(a.epi_mode, __uint_as_float(y[j]),
+                                               __uint_as_float(ea[j]), __uint_as_float(eb[j])));
+    }
+  }
+  return o;
+}
+
+// Writes an out-projection tile staged in LDS to out (origin (m0, n0)) by the NT
+// threads t0 .. t0 + NT - 1 of the work-group (tid: this thread's index among
+// them), through the fused epilogue a.epi_mode.
 template <class TL, class T, int NT>
-__device__ __forceinline__ void flush_tile_by(const char* stage, T* dst, int64_t ld, int rows_valid,
-                                              int cols_valid, int tid) {
+__device__ __forceinline__ void flush_tile_by(const char* stage, const FwdArgs& a, int64_t m0,
+                                              int64_t n0, int rows_valid, int cols_valid, int tid) {
   constexpr int RB = TileStage<TL, T>::kRowBytes;
   constexpr int CPR = TL::BN * (int)sizeof(T) / 16;
   constexpr int EPC = 16 / (int)sizeof(T);
+  T* dst = reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0;
   for (int c = tid; c < TL::BM * CPR; c += NT) {
     const int row = c / CPR, ch = c - row * CPR;
-    if (row < rows_valid && ch * EPC < cols_valid)
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + row * RB + ch * 16),
-                                  reinterpret_cast<u32x4*>(dst + row * ld + ch * EPC));
+    if (row < rows_valid && ch * EPC < cols_valid) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * RB + ch * 16);
+      if (a.epi_mode != kEpiNone) v = epi_chunk<T>(a, v, m0 + row, n0 + ch * EPC);
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + row * a.d_out + ch * EPC));
+    }
   }
 }
 
@@ -1513,8 +1562,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
   }
   stage_tile<TL, T>(acc, stage, bcol, scol);
   __syncthreads();
-  flush_tile<TL, T>(stage, reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0, a.d_out, rows_valid,
-                    cols_valid);
+  flush_tile_by<TL, T, TL::kThreads>(stage, a, m0, n0, rows_valid, cols_valid, (int)threadIdx.x);
 }
 
 // Persistent bf16 out-projection (8 waves, ping-pong main loop): work-group b
@@ -1549,8 +1597,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
     wait_vm_lds<63>();   // LDS writes done; stores of the previous tile may still drain
     lds_barrier();
     if (grp == 1)
-      flush_tile_by<TL, T, 256>(stage, reinterpret_cast<T*>(a.out) + m0 * a.d_out + n0, a.d_out,
-                                rows_valid, cols_valid, (int)threadIdx.x - 256);
+      flush_tile_by<TL, T, 256>(stage, a, m0, n0, rows_valid, cols_valid,
+                                (int)threadIdx.x - 256);
     wait_vm_lds<63>();   // the staged tile is read before the next tile's DMA reuses it
     lds_barrier();
   }
@@ -1661,6 +1709,30 @@ __global__ void k_copy_pad(const T* __restrict__ src, T* __restrict__ dst, int64
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_pad;
        i += (int64_t)gridDim.x * blockDim.x)
     dst[i] = i < n ? src[i] : T(0);
+}
+
+// out[t, :] = (x[t, :] / sqrt(mean(x[t, :]^2) + eps)) * w, computed in fp32 and rounded
+// to T once (model.py:25-27: the sqrt, then the division, then the gain); one wave
+// per row, the sum of squares in lane order then a wave reduction.
+template <class T>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, int64_t n_rows,
+                                                      int64_t d, const T* __restrict__ w, float eps,
+                                                      T* __restrict__ out) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n_rows) return;   // whole waves: no barrier follows
+  const T* xr = x + row * d;
+  float ss = 0.f;
+  for (int64_t i = lane; i < d; i += 64) {
+    const float v = load_as_f32(xr + i);
+    ss += v * v;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float rms = sqrtf(ss / (float)d + eps);
+  T* orow = out + row * d;
+  for (int64_t i = lane; i < d; i += 64)
+    store_from_f32(orow + i, (load_as_f32(xr + i) / rms) * load_as_f32(w + i));
 }
 
 template <class T>

@@ -341,9 +341,15 @@ __global__ __launch_bounds__(64 * W) void k_sk_out(FwdArgs a) {
                              cols_valid, a.r2, red);
   for (int e = threadIdx.x; e < MF * 256; e += 64 * W) {
     const int row = e >> 4;
-    if (row < rows_valid && c < cols_valid)
-      store_from_f32(reinterpret_cast<T*>(a.out) + (m0 + row) * a.d_out + n0 + c,
-                     red[e] * sc + bias);
+    if (row < rows_valid && c < cols_valid) {
+      const int64_t oi = (m0 + row) * a.d_out + n0 + c;
+      float y = red[e] * sc + bias;
+      if (a.epi_mode != kEpiNone)   // the fused FFN epilogue on the rounded layer output
+        y = epi_value<Elt>(a.epi_mode, round_as(y, Elt{}), load_as_f32(static_cast<const T*>(a.epi_a) + oi),
+                           a.epi_mode == kEpiResScale
+                               ? load_as_f32(static_cast<const T*>(a.epi_b) + n0 + c) : 0.f);
+      store_from_f32(reinterpret_cast<T*>(a.out) + oi, y);
+    }
   }
 }
 

@@ -39,12 +39,33 @@ from . import fp8 as _fp8
 
 
 class RMSNorm(nn.Module):
-    """Holds inner_norm.weight and eps (model.py:19-27); applied inside the kernels."""
+    """RMSNorm (model.py:19-27): weight (dim) and eps.
+
+    As TuckerMoE.inner_norm it only holds its parameters (the kernels apply it).
+    Called, it computes (x / sqrt(mean(x^2) + eps)) * weight over the last axis
+    with tmoe_rmsnorm_rows (fp32 arithmetic, one rounding to x's dtype); HIP
+    devices only, x and weight of one dtype (bf16 or fp32)."""
 
     def __init__(self, dim: int, eps: float = 1e-5):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(dim))
         self.eps = eps
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        d = self.weight.shape[0]
+        if x.device.type != "cuda":
+            raise RuntimeError(f"RMSNorm runs on HIP devices only; input is on {x.device}")
+        if x.shape[-1] != d or x.dtype != self.weight.dtype:
+            raise RuntimeError(f"RMSNorm: input (..., {x.shape[-1]}) {x.dtype}, weight ({d}) "
+                               f"{self.weight.dtype}")
+        dt = _lib.dtype_code(x.dtype)
+        X = x.reshape(-1, d).contiguous()
+        y = torch.empty_like(X) if out is None else out
+        with torch.cuda.device(X.device):
+            _lib.check(_lib.lib().tmoe_rmsnorm_rows(
+                X.data_ptr(), X.shape[0], d, self.weight.data_ptr(), float(self.eps), dt,
+                y.data_ptr(), torch.cuda.current_stream(X.device).cuda_stream))
+        return y.reshape(x.shape)
 
 
 class TuckerMoE(nn.Module):
@@ -234,6 +255,16 @@ class TuckerMoE(nn.Module):
         topk_idx / topk_w are the values model.py:76-77 computes (indices in
         descending logit order); they and `logits` are None unless requested.
         """
+        return self.forward_raw(x, routing=routing, logits=logits)
+
+    def forward_raw(self, x: torch.Tensor, routing: bool = False, logits: bool = False,
+                    epi: int = 0, epi_a: Optional[torch.Tensor] = None,
+                    epi_b: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+        """forward_with_routing with a fused epilogue (tmoe_forward_epi): epi is
+        _lib.TMOE_EPI_NONE / _GLU (out = silu(epi_a) * y) / _RESIDUAL_SCALE
+        (out = epi_a + epi_b * y), y = this layer's output; epi_a (..., d_out) and
+        epi_b (d_out) in the parameter dtype. `out` (T, d_out), which may be
+        epi_a itself, receives the result."""
         *batch, d_in = x.shape
         dtype = self.U_in.dtype
         if x.device.type != "cuda":
@@ -253,7 +284,23 @@ class TuckerMoE(nn.Module):
         plan = self.plan()
         packed = self.packed()
         dev = X.device
-        out = torch.empty(T, d_out, dtype=dtype, device=dev)
+        if out is None:
+            out = torch.empty(T, d_out, dtype=dtype, device=dev)
+        elif (out.shape != (T, d_out) or out.dtype != dtype or out.device != dev
+              or not out.is_contiguous()):
+            raise RuntimeError(f"TuckerMoE: out must be a contiguous ({T}, {d_out}) {dtype} tensor")
+        ea = eb = None
+        if epi != _lib.TMOE_EPI_NONE:
+            ea = epi_a.reshape(T, d_out) if epi_a is not None else None
+            if ea is None or ea.dtype != dtype or ea.device != dev or not ea.is_contiguous():
+                raise RuntimeError(f"TuckerMoE: epi_a must be a contiguous ({T}, {d_out}) "
+                                   f"{dtype} tensor on {dev}")
+        if epi == _lib.TMOE_EPI_RESIDUAL_SCALE:
+            eb = epi_b
+            if (eb is None or eb.shape != (d_out,) or eb.dtype != dtype or eb.device != dev
+                    or not eb.is_contiguous()):
+                raise RuntimeError(f"TuckerMoE: epi_b must be a contiguous ({d_out},) {dtype} "
+                                   f"tensor on {dev}")
         idx = torch.empty(T, self.top_k, dtype=torch.int32, device=dev) if routing else None
         w = torch.empty(T, self.top_k, dtype=torch.float32, device=dev) if routing else None
         lg = torch.empty(T, E, dtype=torch.float32, device=dev) if logits else None
@@ -261,12 +308,13 @@ class TuckerMoE(nn.Module):
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             stream = torch.cuda.current_stream(dev).cuda_stream
-            _lib.check(_lib.lib().tmoe_forward(
+            _lib.check(_lib.lib().tmoe_forward_epi(
                 plan.ptr, X.data_ptr(), T, packed.data_ptr(), out.data_ptr(),
                 idx.data_ptr() if idx is not None else None,
                 w.data_ptr() if w is not None else None,
                 lg.data_ptr() if lg is not None else None,
-                ws.data_ptr(), ws_bytes, stream))
+                ws.data_ptr(), ws_bytes, epi, ea.data_ptr() if ea is not None else None,
+                eb.data_ptr() if eb is not None else None, stream))
         out = out.reshape(*batch, d_out)
         return out, (idx.long() if idx is not None else None), w, lg
 

@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import fp8
-from .config import Workload
+from .config import FfnWorkload, Workload
 
 PARAM_KEYS = ("router.weight", "U_in", "inner_norm.weight", "U_expert", "core", "U_out", "bias")
 _IDS = {k: i + 1 for i, k in enumerate(PARAM_KEYS)}
@@ -89,6 +89,34 @@ def make_x(w: Workload, T: int = None, dtype: torch.dtype = None, stream: int = 
     dtype = w.dtype if dtype is None else dtype
     x = _normal(w.seed, _X_ID + stream, (T, w.d_in), 1.0)
     return round_to(torch.from_numpy(x), dtype)
+
+
+_FFN_NORM_ID, _FFN_GAMMA_ID = 200, 201
+
+
+def make_ffn_params(f: FfnWorkload, affine: str = "random",
+                    dtype: torch.dtype = None) -> Dict[str, torch.Tensor]:
+    """CPU tensors keyed like TransformerBlock.state_dict() restricted to the FFN
+    sub-block: norm_ffn.weight, ffn_gate.*, ffn_up.*, ffn_down.*, ls_ffn.gamma.
+    Each TuckerMoE comes from make_params of f.layer(name); norm_ffn.weight and
+    ls_ffn.gamma are 1 + 0.1 N(0, 1) ("random") or ones ("unit")."""
+    dtype = f.dtype if dtype is None else dtype
+    p = {}
+    for name in ("ffn_gate", "ffn_up", "ffn_down"):
+        for k, v in make_params(f.layer(name), affine=affine, dtype=dtype).items():
+            p[f"{name}.{k}"] = v
+    for key, tid in (("norm_ffn.weight", _FFN_NORM_ID), ("ls_ffn.gamma", _FFN_GAMMA_ID)):
+        v = (1.0 + _normal(f.seed, tid, (f.d,), 0.1) if affine == "random"
+             else np.ones((f.d,), np.float32))
+        p[key] = round_to(torch.from_numpy(np.ascontiguousarray(v)), dtype)
+    return p
+
+
+def make_ffn_x(f: FfnWorkload, T: int = None, dtype: torch.dtype = None) -> torch.Tensor:
+    """(T, d) CPU residual-stream rows ~ N(0, 1) in `dtype`."""
+    T = f.T if T is None else T
+    dtype = f.dtype if dtype is None else dtype
+    return round_to(torch.from_numpy(_normal(f.seed, _X_ID, (T, f.d), 1.0)), dtype)
 
 
 def sha256(t: torch.Tensor) -> str:

@@ -154,3 +154,41 @@ def test_fp8_plan_and_pack_validation(pkg):
         L.tmoe_plan_destroy(pb)
     with pytest.raises(pkg._lib.TmoeError):
         pkg._lib.Plan(512, 1024, 8, 2, 4, 256, 128, torch.float32, 1e-5, fp8_weights=True)
+
+
+def test_forward_epi_and_rmsnorm_validation_never_launch(pkg):
+    """tmoe_forward_epi and tmoe_rmsnorm_rows reject bad epilogue / norm
+    arguments before any HIP call."""
+    rc, p, _ = _create(pkg)
+    L = pkg._lib.lib()
+    lb = pkg._lib
+    fe = L.tmoe_forward_epi
+    ok = 0x10000
+    ws = L.tmoe_workspace_bytes(p, 64)
+    try:
+        assert fe(p, ok, 64, ok, ok, None, None, None, ok, ws, 7, ok, ok, None) == -1
+        assert "epi_mode" in L.tmoe_last_error().decode()
+        assert fe(p, ok, 64, ok, ok, None, None, None, ok, ws, lb.TMOE_EPI_GLU, None, None,
+                  None) == -1
+        assert "epi_a" in L.tmoe_last_error().decode()
+        assert fe(p, ok, 64, ok, ok, None, None, None, ok, ws, lb.TMOE_EPI_GLU, ok + 2, None,
+                  None) == -1
+        assert fe(p, ok, 64, ok, ok, None, None, None, ok, ws, lb.TMOE_EPI_RESIDUAL_SCALE, ok,
+                  None, None) == -1
+        assert "gamma" in L.tmoe_last_error().decode()
+        # argument errors of tmoe_forward are still reported with an epilogue
+        assert fe(p, ok, 64, ok, ok, None, None, None, ok, ws - 1, lb.TMOE_EPI_GLU, ok, None,
+                  None) == -1
+        assert "workspace" in L.tmoe_last_error().decode()
+        assert fe(p, ok, 0, None, None, None, None, None, None, 0, lb.TMOE_EPI_GLU, ok, None,
+                  None) == 0
+    finally:
+        L.tmoe_plan_destroy(p)
+    rn = L.tmoe_rmsnorm_rows
+    assert rn(ok, 4, 64, ok, 1e-5, 5, ok, None) == -1
+    assert "dtype" in L.tmoe_last_error().decode()
+    assert rn(ok, -1, 64, ok, 1e-5, lb.TMOE_BF16, ok, None) == -1
+    assert rn(ok, 4, 0, ok, 1e-5, lb.TMOE_BF16, ok, None) == -1
+    assert rn(ok, 4, 64, ok, -1.0, lb.TMOE_BF16, ok, None) == -1
+    assert rn(ok, 4, 64, None, 1e-5, lb.TMOE_BF16, ok, None) == -1
+    assert rn(None, 0, 64, None, 1e-5, lb.TMOE_BF16, None, None) == 0   # T == 0: no-op
