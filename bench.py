@@ -61,6 +61,120 @@ def traffic_per_launch(workload: str, kernel: str):
     return None
 
 
+FFN_METRIC = "TransformerBlock FFN sub-block tokens/sec (norm, gate, up, silu*up, down, residual)"
+
+
+def bench_ffn(args) -> None:
+    """--ffn NAME: one step = TuckerFFN.forward over T tokens of the FFN workload
+    NAME (model.py:337-341: RMSNorm, three TuckerMoE layers, silu(gate) * up and
+    the LayerScale residual fused into the layers' out-projection stores). The
+    same launches with the two elementwise ops done by separate torch kernels
+    (the reference's op sequence on the GPU) are timed beside it."""
+    import torch
+    import torch.nn.functional as F
+
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    f = pkg.FFN_WORKLOADS[args.ffn]
+    T = args.tokens or f.T
+    dev = torch.device("cuda:0")
+    dt_name = "bf16" if f.dtype == torch.bfloat16 else "f32"
+    es = 2 if f.dtype == torch.bfloat16 else 4
+    params = pkg.synth.make_ffn_params(f)
+    x0 = pkg.synth.make_ffn_x(f, T)
+    m0 = pkg.TuckerFFN(f.d, f.cfg()).to(dev, f.dtype)
+    m0.load_state_dict({k: v.to(dev) for k, v in params.items()})
+    packed = sum(getattr(m0, n).packed().numel() for n in ("ffn_gate", "ffn_up", "ffn_down"))
+    set_bytes = packed + T * f.d * es * 2 + T * f.d_ff * es * 2
+    n_sets = max(3, math.ceil(args.rotate_mb * 1e6 / set_bytes))
+    log(f"[bench-ffn] {f.name}: T={T} d={f.d} d_ff={f.d_ff} E={f.E} k={f.k} "
+        f"r=({f.r1},{f.r3},{f.r2}) {dt_name}; {n_sets} rotated sets x {set_bytes / 1e6:.1f} MB")
+    gen = torch.Generator(device=dev).manual_seed(f.seed)
+    sets = []
+    for i in range(n_sets):
+        if i == 0:
+            m = m0
+        else:
+            m = pkg.TuckerFFN(f.d, f.cfg()).to(dev, f.dtype)
+            m.load_state_dict(m0.state_dict())
+        for n in ("ffn_gate", "ffn_up", "ffn_down"):
+            getattr(m, n).packed()
+        x = x0.to(dev) if i == 0 else torch.randn(T, f.d, device=dev, generator=gen).to(f.dtype)
+        sets.append((m, x))
+
+    def fused(i):
+        m, x = sets[i % n_sets]
+        return m(x)
+
+    def unfused(i):
+        m, x = sets[i % n_sets]
+        x_f = m.norm_ffn(x)
+        h = F.silu(m.ffn_gate(x_f)) * m.ffn_up(x_f)
+        return x + m.ls_ffn.gamma * m.ffn_down(h)
+
+    def timed(fn):
+        with torch.no_grad():
+            for i in range(args.warmup):
+                fn(i)
+            torch.cuda.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            for i in range(args.steps):
+                fn(i)
+            ev1.record()
+            torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / args.steps
+
+    ms = timed(fused)
+    ms_unfused = timed(unfused)
+    tok_s = T / (ms * 1e-3)
+    flops = sum(f.layer(n).flops(T)["total"] for n in ("ffn_gate", "ffn_up", "ffn_down"))
+    peak = PEAK_TFLOPS[dt_name]
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"[bench-ffn] fused {ms * 1e3:.1f} us/step ({tok_s / 1e6:.2f} M tok/s, {tflops:.0f} "
+        f"TFLOP/s); separate elementwise kernels {ms_unfused * 1e3:.1f} us/step")
+
+    from oracle import tucker_ffn_torch as ft
+    from oracle import tucker_moe_np as onp
+    n_par = min(T, 256)
+    with torch.no_grad():
+        y = fused(0)
+    torch.cuda.synchronize()
+    ref = ft.ffn_forward(x0[:n_par], params, f.k, compute_dtype=torch.float32)
+    parity = {"tokens": n_par,
+              "rel_l2_out": onp.rel_l2(y[:n_par].float().cpu().numpy(), ref.double().numpy()),
+              "reference": "oracle/tucker_ffn_torch fp32 on the bf16-valued inputs "
+                           "(rows that route differently included)"}
+    cpu = None
+    if not args.no_cpu:
+        threads = torch.get_num_threads()
+        chunk = min(256, T)
+        t_a = time.perf_counter()
+        ft.ffn_forward(x0[:chunk], params, f.k, chunk=chunk)
+        rate = chunk / (time.perf_counter() - t_a)
+        n_cpu = int(min(T, max(chunk, args.cpu_seconds * rate)) // chunk * chunk)
+        t_a = time.perf_counter()
+        ft.ffn_forward(x0[:n_cpu], params, f.k, chunk=chunk)
+        cpu_s = time.perf_counter() - t_a
+        cpu = {"value": n_cpu / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": (f"first {n_cpu} of the {T} {f.name} tokens, {dt_name}, the reference "
+                          f"op sequence (oracle/tucker_ffn_torch), torch {torch.__version__} "
+                          f"with {threads} threads on {cpu_model()}"),
+               "seconds": cpu_s}
+    print(json.dumps({
+        "metric": FFN_METRIC, "value": tok_s, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dt_name,
+        "data": "synthetic (seeded N(0,1) tokens, N(0,1/fan_in) weights; no checkpoint)",
+        "config": {"workload": f"{f.name}: TransformerBlock FFN sub-block, one GPU", "T": T,
+                   "d": f.d, "d_ff": f.d_ff, "E": f.E, "top_k": f.k, "r1": f.r1, "r3": f.r3,
+                   "r2": f.r2, "rotated_sets": n_sets},
+        "mfma": {"tflops": tflops, "peak": peak, "frac": tflops / peak, "flops_per_step": flops},
+        "separate_elementwise_ms_per_step": ms_unfused,
+        "parity": parity, "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -76,6 +190,8 @@ def main():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the timed work, copy a buffer of this many MiB 3 times (a plain "
                          "copy kernel of known size, to scale profiler byte counters)")
+    ap.add_argument("--ffn", default=None,
+                    help="time the FFN sub-block of this FFN workload (F0, F1, F2) instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -83,6 +199,9 @@ def main():
               "build (the layer shards by tokens with no exchange; see the design notes).",
               file=sys.stderr)
         sys.exit(2)
+    if args.ffn:
+        bench_ffn(args)
+        return
 
     import numpy as np
     import torch

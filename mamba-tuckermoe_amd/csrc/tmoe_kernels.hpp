@@ -667,9 +667,12 @@ __device__ __forceinline__ void flush_tile(const char* stage, T* dst, int64_t ld
 // one row, stored as one 8-byte LDS write of (acc * scale + bias). Columns are
 // cut at multiples of 16 only, so a group of four is wholly valid or not. bias
 // and scale point at the tile's first column and are 16-byte aligned.
+// With gamma (bf16, the tile's first column; kEpiResScale), each staged value is
+// R(gamma[col] * R(y)) instead of R(y): the scaled half of the residual epilogue.
 template <class TL>
 __device__ __forceinline__ void stage_tile_t(const f32x16 (&acc)[TL::FM][TL::FN], char* stage,
-                                             const float* bias, const float* scale, int cols_valid) {
+                                             const float* bias, const float* scale, int cols_valid,
+                                             const uint16_t* gamma = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
   constexpr int RB = TileStage<TL, uint16_t>::kRowBytes;
@@ -683,6 +686,7 @@ __device__ __forceinline__ void stage_tile_t(const f32x16 (&acc)[TL::FM][TL::FN]
       const float4 bv = *reinterpret_cast<const float4*>(bias + cc);
       const float4 sv = scale ? *reinterpret_cast<const float4*>(scale + cc)
                               : float4{1.f, 1.f, 1.f, 1.f};
+      const uint2 gv = gamma ? *reinterpret_cast<const uint2*>(gamma + cc) : uint2{0u, 0u};
 #pragma unroll
       for (int i = 0; i < TL::FM; ++i) {
         const int row = wm * TL::kWaveM + i * 32 + (lane & 31);
@@ -690,6 +694,12 @@ __device__ __forceinline__ void stage_tile_t(const f32x16 (&acc)[TL::FM][TL::FN]
         v.x = pack_bf16x2(acc[i][j][4 * q] * sv.x + bv.x, acc[i][j][4 * q + 1] * sv.y + bv.y);
         v.y = pack_bf16x2(acc[i][j][4 * q + 2] * sv.z + bv.z,
                           acc[i][j][4 * q + 3] * sv.w + bv.w);
+        if (gamma) {
+          v.x = pack_bf16x2(bf16_bits_to_f32(gv.x & 0xffffu) * bf16_bits_to_f32(v.x & 0xffffu),
+                            bf16_bits_to_f32(gv.x >> 16) * bf16_bits_to_f32(v.x >> 16));
+          v.y = pack_bf16x2(bf16_bits_to_f32(gv.y & 0xffffu) * bf16_bits_to_f32(v.y & 0xffffu),
+                            bf16_bits_to_f32(gv.y >> 16) * bf16_bits_to_f32(v.y >> 16));
+        }
         *reinterpret_cast<uint2*>(stage + row * RB + col * 2) = v;
       }
     }
@@ -703,13 +713,22 @@ __device__ __forceinline__ void stage_tile_t(const f32x16 (&acc)[TL::FM][TL::FN]
 //   kEpiResScale  out = R(x + R(gamma[col] * y)), x = epi_a[row, col], gamma = epi_b
 //                                                    x_res + ls_ffn(dn)   (:35-36, :341)
 // R rounds to the module dtype, as each of the reference module's ops does;
-// silu(g) = g / (1 + exp(-g)) in fp32.
+// silu(g) = g / (1 + exp(-g)) in fp32 (see silu_as).
 __device__ __forceinline__ float round_as(float v, EltBF16) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 __device__ __forceinline__ float round_as(float v, EltF32) { return v; }
+// silu(g) before rounding to the dtype. fp32: g / (1 + expf(-g)). bf16: g times
+// the hardware reciprocal of 1 + 2^(-g log2 e) (v_exp_f32, v_rcp_f32; a few fp32
+// units in the last place, which the rounding to bf16 absorbs but for about one
+// element in 10^4, then one bf16 unit apart). Limits: g -> -inf gives -0, g ->
+// +inf gives g, NaN stays NaN.
+__device__ __forceinline__ float silu_as(float g, EltF32) { return g / (1.f + expf(-g)); }
+__device__ __forceinline__ float silu_as(float g, EltBF16) {
+  return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.44269504f));
+}
 template <class Elt>
 __device__ __forceinline__ float epi_value(int mode, float y, float ea, float eb) {
 #pragma clang fp contract(off)   // x + gamma * y is two rounded ops, as in the reference
-  if (mode == kEpiGlu) return round_as(round_as(ea / (1.f + expf(-ea)), Elt{}) * y, Elt{});
+  if (mode == kEpiGlu) return round_as(round_as(silu_as(ea, Elt{}), Elt{}) * y, Elt{});
   return round_as(ea + round_as(eb * y, Elt{}), Elt{});
 }
 // epi_value over one 16-byte chunk y of output row `row`, columns col .. col + 16 /
@@ -740,10 +759,60 @@ __device__ __forceinline__ u32x4 epi_chunk(const FwdArgs& a, u32x4 y, int64_t ro
   return o;
 }
 
+// Applies the fused epilogue to a bf16 tile staged in LDS, in place, by NT
+// threads: each thread takes chunks tid, tid + NT, ... and loads their epi_a
+// values in batches of kBatch before combining and writing them back (one wait
+// per batch). Only loads are issued here, so a wave that never stores keeps its
+// vector-memory counter free of stores. For kEpiResScale the stage holds
+// R(gamma * y) already (stage_tile_t); out = R(x + that). For kEpiGlu out =
+// R(R(silu(g)) * y).
+template <class TL, int NT, int kBatch>
+__device__ __forceinline__ void epi_tile_in_lds(char* stage, const FwdArgs& a, int64_t m0,
+                                                int64_t n0, int rows_valid, int cols_valid,
+                                                int tid) {
+  constexpr int RB = TileStage<TL, uint16_t>::kRowBytes;
+  constexpr int CPR = TL::BN * 2 / 16;
+  constexpr int kIters = TL::BM * CPR / NT;
+  static_assert(TL::BM * CPR % NT == 0 && kIters % kBatch == 0, "whole batches");
+  const uint16_t* ea = static_cast<const uint16_t*>(a.epi_a) + m0 * a.d_out + n0;
+  const bool glu = a.epi_mode == kEpiGlu;
+  // opaque copy: the chunk offsets below are recomputed per tile rather than
+  // hoisted out of a persistent tile loop (where they would be spilled)
+  asm volatile("" : "+v"(tid));
+  for (int b = 0; b < kIters; b += kBatch) {
+    u32x4 e[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = tid + (b + i) * NT, row = c / CPR, ch = c - row * CPR;
+      e[i] = u32x4{0u, 0u, 0u, 0u};
+      if (row < rows_valid && ch * 8 < cols_valid)
+        e[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(ea + row * a.d_out + ch * 8));
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = tid + (b + i) * NT, row = c / CPR, ch = c - row * CPR;
+      u32x4* slot = reinterpret_cast<u32x4*>(stage + row * RB + ch * 16);
+      const u32x4 y = *slot;
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float y0 = bf16_bits_to_f32(y[j] & 0xffffu), y1 = bf16_bits_to_f32(y[j] >> 16);
+        const float e0 = bf16_bits_to_f32(e[i][j] & 0xffffu), e1 = bf16_bits_to_f32(e[i][j] >> 16);
+        o[j] = glu ? pack_bf16x2(round_as(silu_as(e0, EltBF16{}), EltBF16{}) * y0,
+                                 round_as(silu_as(e1, EltBF16{}), EltBF16{}) * y1)
+                   : pack_bf16x2(e0 + y0, e1 + y1);
+      }
+      *slot = o;
+    }
+  }
+}
+
 // Writes an out-projection tile staged in LDS to out (origin (m0, n0)) by the NT
 // threads t0 .. t0 + NT - 1 of the work-group (tid: this thread's index among
-// them), through the fused epilogue a.epi_mode.
-template <class TL, class T, int NT>
+// them), through the fused epilogue a.epi_mode unless kStagedFinal (the stage
+// holds the final values already, epi_tile_in_lds).
+template <class TL, class T, int NT, bool kStagedFinal = false>
 __device__ __forceinline__ void flush_tile_by(const char* stage, const FwdArgs& a, int64_t m0,
                                               int64_t n0, int rows_valid, int cols_valid, int tid) {
   constexpr int RB = TileStage<TL, T>::kRowBytes;
@@ -754,7 +823,7 @@ __device__ __forceinline__ void flush_tile_by(const char* stage, const FwdArgs& 
     const int row = c / CPR, ch = c - row * CPR;
     if (row < rows_valid && ch * EPC < cols_valid) {
       u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * RB + ch * 16);
-      if (a.epi_mode != kEpiNone) v = epi_chunk<T>(a, v, m0 + row, n0 + ch * EPC);
+      if (!kStagedFinal && a.epi_mode != kEpiNone) v = epi_chunk<T>(a, v, m0 + row, n0 + ch * EPC);
       __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + row * a.d_out + ch * EPC));
     }
   }
@@ -1569,6 +1638,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
 // takes tiles b, b + gridDim.x, ... Each tile is staged in LDS by all waves and
 // written out by group 1 alone, whose stores then drain during the next tile's
 // main loop (group 1 never waits on vmcnt; group 0 issues every DMA).
+constexpr int kOutEpiBatch = 12;    // epilogue chunks per thread loaded at once
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
   typedef uint16_t T;
@@ -1593,12 +1663,22 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
     f32x16 acc[TL::FM][TL::FN];
     gemm_mainloop_pingpong<TL, EltBF16>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem);
     stage_tile_t<TL>(acc, stage, a.bias + n0, a.out_scale ? a.out_scale + n0 : nullptr,
-                     cols_valid);
+                     cols_valid,
+                     a.epi_mode == kEpiResScale ? static_cast<const uint16_t*>(a.epi_b) + n0
+                                                : nullptr);
     wait_vm_lds<63>();   // LDS writes done; stores of the previous tile may still drain
     lds_barrier();
+    if (a.epi_mode != kEpiNone) {
+      // all 8 waves apply the epilogue in LDS (group 0 only loads); then group 1
+      // stores the tile as for a plain one
+      epi_tile_in_lds<TL, 512, kOutEpiBatch>(stage, a, m0, n0, rows_valid, cols_valid,
+                                             (int)threadIdx.x);
+      wait_vm_lds<63>();
+      lds_barrier();
+    }
     if (grp == 1)
-      flush_tile_by<TL, T, 256>(stage, a, m0, n0, rows_valid, cols_valid,
-                                (int)threadIdx.x - 256);
+      flush_tile_by<TL, T, 256, true>(stage, a, m0, n0, rows_valid, cols_valid,
+                                      (int)threadIdx.x - 256);
     wait_vm_lds<63>();   // the staged tile is read before the next tile's DMA reuses it
     lds_barrier();
   }
