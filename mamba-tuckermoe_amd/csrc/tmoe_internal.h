@@ -50,6 +50,8 @@ struct FwdArgs {
   void* z;                      // (T, r3)
   void* mid;                    // (T, r2)
   float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
+  float* mpart;                 // (T_pad, r2) fp32     k_core_pp with r1 > 4: partial sums
+                                //                      over rank groups (null otherwise)
   // elementwise op fused into the out-projection's store (kEpi*): the FFN
   // sub-block's silu(gate) * up, or its residual + LayerScale
   int epi_mode;
@@ -65,12 +67,17 @@ constexpr int64_t kSmallT = 256;
 
 // k_core_pp (the persistent core for bf16 plans): ranks r1 in {1, 2, 4}, r1 * r2 a
 // multiple of its 256-row tiles, and for fp8 weights at most kCorePScales channel
-// scales (staged in LDS). Its 256-token tiles store whole tiles of mid, so the
-// workspace holds mid for T rounded up to kCorePRows rows.
+// scales (staged in LDS); or, bf16 weights only, r1 = 4 G (G > 1) with r2 a
+// multiple of 64, in rank groups of 4 (partial sums in the workspace's mpart).
+// Its 256-token tiles store whole tiles of mid, so the workspace holds mid for T
+// rounded up to kCorePRows rows.
 constexpr int kCorePRows = 256;
 constexpr int64_t kCorePScales = 4096;
+inline bool core_p_grouped(int64_t r1) { return r1 > 4; }
 inline bool core_p_supported(int64_t r1, int64_t r2, bool bf16, bool fp8w) {
-  return bf16 && (r1 == 1 || r1 == 2 || r1 == 4) && (r1 * r2) % 256 == 0 &&
+  if (!bf16) return false;
+  if (core_p_grouped(r1)) return r1 % 4 == 0 && r2 % 64 == 0 && !fp8w;
+  return (r1 == 1 || r1 == 2 || r1 == 4) && (r1 * r2) % 256 == 0 &&
          (!fp8w || r1 * r2 <= kCorePScales);
 }
 

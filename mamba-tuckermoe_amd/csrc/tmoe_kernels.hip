@@ -68,8 +68,8 @@ hipError_t launch_front_t(const FwdArgs& a, hipStream_t st) {
   }
 }
 
-// Persistent core: one work-group per compute unit, at most one per tile.
-template <int R1>
+// Persistent core: one work-group per compute unit, at most one per output tile.
+template <int R1, bool kGrouped = false>
 hipError_t launch_core_pp_r(const FwdArgs& a, hipStream_t st);
 
 template <class Elt, class C>
@@ -111,12 +111,13 @@ hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int R1>
+template <int R1, bool kGrouped>
 hipError_t launch_core_pp_r(const FwdArgs& a, hipStream_t st) {
-  const int64_t tiles = (int64_t)cdiv(a.T, kCorePRows) * (a.r1 * a.r2 / 256);
+  // output tiles (each of r1 / R1 rank groups)
+  const int64_t tiles = (int64_t)cdiv(a.T, kCorePRows) * (R1 * a.r2 / 256);
   const int64_t ncu = cu_count();
   const dim3 grid((unsigned)(tiles < ncu ? tiles : ncu)), block(512);
-  hipLaunchKernelGGL((dev::k_core_pp<R1, kCorePSteps>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((dev::k_core_pp<R1, kCorePSteps, kGrouped>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
@@ -184,7 +185,9 @@ hipError_t launch_core(const FwdArgs& a, hipStream_t st) {
       case 1: return launch_core_pp_r<1>(a, st);
       case 2: return launch_core_pp_r<2>(a, st);
       case 4: return launch_core_pp_r<4>(a, st);
-      default: return hipErrorInvalidValue;
+      default:
+        if (core_p_grouped(a.r1) && a.mpart) return launch_core_pp_r<4, true>(a, st);
+        return hipErrorInvalidValue;
     }
   }
   return a.dtype == kDtypeBF16 ? launch_core_t<EltBF16, CoreCfgBF16>(a, st)
@@ -254,6 +257,21 @@ hipError_t launch_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* 
                                int dtype, void* out, hipStream_t st) {
   if (T == 0) return hipSuccess;
   const dim3 grid(cdiv(T, 4)), block(256);
+  const int es = dtype == kDtypeBF16 ? 2 : 4;
+  const bool vec = (d * es) % 16 == 0 && d * es <= 64 * 8 * 16 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                     reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  if (vec) {   // rows of at most 8 KB, held in registers
+    if (dtype == kDtypeBF16)
+      hipLaunchKernelGGL((dev::k_rmsnorm_rows_v<uint16_t, 8>), grid, block, 0, st,
+                         static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w),
+                         eps, static_cast<uint16_t*>(out));
+    else
+      hipLaunchKernelGGL((dev::k_rmsnorm_rows_v<float, 8>), grid, block, 0, st,
+                         static_cast<const float*>(x), T, d, static_cast<const float*>(w), eps,
+                         static_cast<float*>(out));
+    return hipGetLastError();
+  }
   if (dtype == kDtypeBF16)
     hipLaunchKernelGGL(dev::k_rmsnorm_rows<uint16_t>, grid, block, 0, st,
                        static_cast<const uint16_t*>(x), T, d, static_cast<const uint16_t*>(w), eps,

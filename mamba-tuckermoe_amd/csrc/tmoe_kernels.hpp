@@ -1378,14 +1378,20 @@ __global__ __launch_bounds__(64 * WM * WN) void k_core(FwdArgs a) {
 // reduces its accumulators over r and stores its part of mid straight from
 // registers (8 bytes a lane; group 0, the DMA issuer, after its wait for the
 // next K tile), then starts the next tile with zeroed
-// accumulators. SPP K steps of a K tile are read per memory phase (2: two
+// accumulators. With r1 = 4 G, G > 1 (R1 = 4), P^T holds the ranks in groups
+// of 4 (row ((g * nqb + qb) * 4 + rr) * 32 + qq) and an output tile (256 tokens x
+// 64 channels) takes G consecutive tiles of the work-group, one per rank group:
+// the reduction over each group's 4 ranks is added to the fp32 partial sum of
+// the groups before it, carried in a.mpart (each lane reads back what it wrote),
+// and the last group stores mid. SPP K steps of a K tile are read per memory phase (2: two
 // memory/compute phase pairs per K tile, which halves the fragment registers).
 // A tile's rows of c reach LDS by DMA with its first K tile (three buffers: the
 // second group still reads tile i - 1's while tile i + 1's lands), so the
 // epilogue issues no global load and waits on nothing. The stores are
 // unconditional: the workspace holds mid for whole 256-row tiles.
-template <int R1, int SPP>
+template <int R1, int SPP, bool kGrouped = false>
 __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
+  static_assert(!kGrouped || R1 == 4, "rank groups of 4");
   typedef Tile<256, 256, 0, 4, 2, 1, 1, 2, true, true> TL;
   constexpr int FM = TL::FM, FN = TL::FN;   // 2 x 4 blocks of 32 x 32
   static_assert(FN % R1 == 0, "rank blocks per wave");
@@ -1409,12 +1415,13 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
   const int64_t r2 = a.r2, r3 = a.r3;
-  const int ntn = (int)(R1 * r2 / TL::BN);
+  const int G = kGrouped ? (int)(a.r1 / R1) : 1;   // rank groups per output tile
+  const int ntn = (int)(R1 * r2 / TL::BN);       // tiles per token tile and rank group
   const int ntm = (int)((a.T + TL::BM - 1) / TL::BM);
-  const int ntiles = ntm * ntn;
-  const int nkt = (int)(r3 * 2 / kTileKBytes);   // K tiles per output tile
-  const int my_tiles = ((int)blockIdx.x < ntiles) ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
-  const int total = my_tiles * nkt;
+  const int nout = ntm * ntn;                    // output tiles
+  const int nkt = (int)(r3 * 2 / kTileKBytes);   // K tiles per tile
+  const int my_out = ((int)blockIdx.x < nout) ? (nout - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = my_out * G * nkt;
   const int64_t row_bytes = r3 * 2;
   const int kt_rot = ((int)blockIdx.x >> 3) % nkt;
   const bool fp8 = a.core_scale_raw != nullptr;
@@ -1422,13 +1429,17 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
     for (int i = tid; i < R1 * (int)r2; i += 512) sc_lds[i] = a.core_scale_raw[i];
   }
 
-  auto coords = [&](int i, int& tm, int& tn) __attribute__((always_inline)) {
-    tile_coords_of((int)blockIdx.x + i * (int)gridDim.x, ntn, ntiles, tm, tn);
+  // tile i of this work-group: output tile o = blockIdx.x + (i / G) gridDim.x (token
+  // tile tm, channel tile tn) and rank group rg = i % G
+  auto coords = [&](int i, int& tm, int& tn, int& rg, int& o) __attribute__((always_inline)) {
+    o = (int)blockIdx.x + (i / G) * (int)gridDim.x;
+    rg = i % G;
+    tile_coords_of(o, ntn, nout, tm, tn);
   };
   // DMA of K tile g of this work-group's stream into `stage` (group 0's waves)
   auto dma_g = [&](int g, int stage) __attribute__((always_inline)) {
-    int tm, tn;
-    coords(g / nkt, tm, tn);
+    int tm, tn, rg, ot;
+    coords(g / nkt, tm, tn, rg, ot);
     // work-groups on one XCD start their tiles' K loops at different K tiles:
     // they read the same P^T rows, and reading the same lines at the same moment
     // measured 20% slower (the sum's order per output element is fixed per tile)
@@ -1436,14 +1447,17 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
     const int64_t m0 = (int64_t)tm * TL::BM;
     const int rows_valid = (int)(a.T - m0 < TL::BM ? a.T - m0 : TL::BM);
     RowLoader al{reinterpret_cast<const char*>(a.z) + m0 * row_bytes, row_bytes, rows_valid};
-    RowLoader bl{reinterpret_cast<const char*>(a.coreP) + (int64_t)tn * TL::BN * row_bytes,
+    RowLoader bl{reinterpret_cast<const char*>(a.coreP) +
+                     (int64_t)(rg * ntn + tn) * TL::BN * row_bytes,
                  row_bytes, TL::BN};
     if (g % nkt == 0 && wave < kCDma) {
-      // 16 bytes of the tile's c rows a lane; the workspace holds c for whole
-      // tiles (rows past T are never used for an output row below T)
+      // 16 bytes of the tile's c rows a lane (with G > 1: row wave * 64 + lane,
+      // ranks 4 rg .. 4 rg + 3); the workspace holds c for whole tiles (rows past T
+      // are never used for an output row below T)
       const int i = g / nkt;
-      const int64_t f = (int64_t)wave * 256 + lane * 4;   // float index within the tile
-      __builtin_amdgcn_global_load_lds((gbl_cvptr)(a.c + m0 * R1 + f),
+      const float* src = G == 1 ? a.c + m0 * R1 + (int64_t)wave * 256 + lane * 4
+                                : a.c + (m0 + wave * 64 + lane) * a.r1 + rg * R1;
+      __builtin_amdgcn_global_load_lds((gbl_cvptr)src,
                                        (lds_vptr)(c_lds + (i % 3) * kCBuf + wave * 256), 16, 0, 0);
     }
     u32x4* s = smem + stage * TL::kStage;
@@ -1472,9 +1486,14 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
   // channels 8 u + 4 (l >> 5) .. + 3 of each column block)
   auto epilogue = [&](int i, auto fp8_tag) __attribute__((always_inline)) {
     constexpr bool kFp8 = decltype(fp8_tag)::value;
-    int tm, tn;
-    coords(i, tm, tn);
+    int tm, tn, rg, ot;
+    coords(i, tm, tn, rg, ot);
     const int64_t m0 = (int64_t)tm * TL::BM;
+    // rank groups: this lane's partial sums, float4 (f, u) of wave `wave` of output tile ot
+    float4* part = G > 1 ? reinterpret_cast<float4*>(a.mpart) +
+                               (((int64_t)ot * 8 + wave) * FM * 4) * 64 + lane
+                         : nullptr;
+    const bool carry_in = G > 1 && rg > 0, carry_out = G > 1 && rg < G - 1;
 #pragma unroll
     for (int g = 0; g < QG; ++g) {
       // channel block of column blocks g * R1 .. g * R1 + R1 - 1 of this wave
@@ -1484,6 +1503,11 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
         // one row block at a time (the scheduler would otherwise interleave the
         // blocks and spill)
         __builtin_amdgcn_sched_barrier(0);
+        float4 pin[4];
+        if (carry_in) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) pin[u] = part[(f * 4 + u) * 64];
+        }
         float cf[R1];
 #pragma unroll
         for (int r = 0; r < R1; ++r)
@@ -1504,6 +1528,16 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
             }
             o[v] = sum;
           }
+          if (carry_in) {
+            o[0] += pin[u].x;
+            o[1] += pin[u].y;
+            o[2] += pin[u].z;
+            o[3] += pin[u].w;
+          }
+          if (carry_out) {
+            part[(f * 4 + u) * 64] = float4{o[0], o[1], o[2], o[3]};
+            continue;
+          }
           uint2 pk;
           pk.x = pack_bf16x2(o[0], o[1]);
           pk.y = pack_bf16x2(o[2], o[3]);
@@ -1517,6 +1551,7 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
                                       8 * (lane >> 5)) = pk;
           }
         }
+        if (carry_out) continue;
         if constexpr (!kFp8) {
           // the block's 32 rows x 32 channels leave as row-contiguous 64-byte pieces,
           // 16 rows a store instead of 32 rows of 16 bytes (LDS operations of one
@@ -1739,10 +1774,12 @@ __global__ void k_transpose_e4m3(const uint8_t* __restrict__ src, uint16_t* __re
   }
 }
 
-// P^T of k_core_pp from core (r1, r3, r2): row (qb * r1 + r) * 32 + qq, column s
-// holds core[r, s, 32 qb + qq]. Source bf16 bits (codes == false) or e4m3 codes
-// with per-channel scales sc (r1, r2), a channel whose scale is zero packed as
-// zeros. One work-group per (channel block qb, 32 columns s, rank r).
+// P^T of k_core_pp from core (r1, r3, r2): with R = min(r1, 4) ranks per group and
+// rank r = R g + rr, row ((g * nqb + qb) * R + rr) * 32 + qq (nqb = r2 / 32), column
+// s holds core[r, s, 32 qb + qq] (for r1 <= 4: row (qb * r1 + r) * 32 + qq). Source
+// bf16 bits (codes == false) or e4m3 codes with per-channel scales sc (r1, r2), a
+// channel whose scale is zero packed as zeros. One work-group per (channel block
+// qb, 32 columns s, rank r).
 template <bool kE4M3>
 __global__ void k_pack_core_p(const void* __restrict__ src, uint16_t* __restrict__ dst,
                               int64_t r1, int64_t r3, int64_t r2, const float* __restrict__ sc) {
@@ -1761,7 +1798,9 @@ __global__ void k_pack_core_p(const void* __restrict__ src, uint16_t* __restrict
     t[y][tx] = v;
   }
   __syncthreads();
-  for (int y = ty; y < 32; y += 8) dst[((qb * r1 + r) * 32 + y) * r3 + s0 + tx] = t[tx][y];
+  const int64_t R = r1 < 4 ? r1 : 4, nqb = r2 / 32;
+  const int64_t prow = (((r / R) * nqb + qb) * R + r % R) * 32;
+  for (int y = ty; y < 32; y += 8) dst[(prow + y) * r3 + s0 + tx] = t[tx][y];
 }
 
 // Core scale table of CoreRescale from sc (r1, r2): cs[r, q] = sc'[r, q] /
@@ -1813,6 +1852,53 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, i
   T* orow = out + row * d;
   for (int64_t i = lane; i < d; i += 64)
     store_from_f32(orow + i, (load_as_f32(xr + i) / rms) * load_as_f32(w + i));
+}
+
+// k_rmsnorm_rows for rows of nch = d * sizeof(T) / 16 <= 64 * kMaxChunks 16-byte
+// chunks (16-byte aligned x, w and out): each lane holds chunks lane, lane + 64,
+// ... in registers, so a row is read from memory once, with 16-byte accesses.
+template <class T, int kMaxChunks>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_v(const T* __restrict__ x, int64_t n_rows,
+                                                        int64_t d, const T* __restrict__ w,
+                                                        float eps, T* __restrict__ out) {
+  constexpr int EPC = 16 / (int)sizeof(T);
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n_rows) return;   // whole waves: no barrier follows
+  const int nch = (int)(d / EPC);
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * d);
+  u32x4 v[kMaxChunks];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxChunks; ++k) {
+    const int c = lane + 64 * k;
+    v[k] = c < nch ? __builtin_nontemporal_load(xr + c) : u32x4{0u, 0u, 0u, 0u};
+    const T* e = reinterpret_cast<const T*>(&v[k]);
+#pragma unroll
+    for (int j = 0; j < EPC; ++j) {
+      const float f = load_as_f32(e + j);
+      ss += f * f;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float rms = sqrtf(ss / (float)d + eps);
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w);
+  u32x4* orow = reinterpret_cast<u32x4*>(out + row * d);
+#pragma unroll
+  for (int k = 0; k < kMaxChunks; ++k) {
+    const int c = lane + 64 * k;
+    if (c < nch) {
+      const u32x4 wv = wr[c];
+      u32x4 o;
+      const T* e = reinterpret_cast<const T*>(&v[k]);
+      const T* g = reinterpret_cast<const T*>(&wv);
+      T* oe = reinterpret_cast<T*>(&o);
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) store_from_f32(oe + j, (load_as_f32(e + j) / rms) * load_as_f32(g + j));
+      orow[c] = o;
+    }
+  }
 }
 
 template <class T>

@@ -182,14 +182,17 @@ def test_zero_core_closed_form(pkg, dev, name, T):
         assert d.max() <= 8, d.max()
 
 
-@pytest.mark.parametrize("T", [64, 300])
-def test_rmsnorm_rows(pkg, dev, T):
-    """tmoe_rmsnorm_rows against float64, in both dtypes, d not a multiple of 64."""
+@pytest.mark.parametrize("d", [200, 768, 4096, 4104])
+@pytest.mark.parametrize("T", [64, 301])
+def test_rmsnorm_rows(pkg, dev, T, d):
+    """tmoe_rmsnorm_rows against float64, in both dtypes: rows held in registers
+    (16-byte multiples up to 8 KB) and the general path (d = 200 in bf16,
+    d = 4104)."""
     for dt in (torch.float32, torch.bfloat16):
         g = torch.Generator().manual_seed(T)
-        x = (torch.randn(T, 200, generator=g) * 3).to(dt)
-        w = (1 + 0.1 * torch.randn(200, generator=g)).to(dt)
-        n = pkg.RMSNorm(200, eps=1e-5).to(dev, dt)
+        x = (torch.randn(T, d, generator=g) * 3).to(dt)
+        w = (1 + 0.1 * torch.randn(d, generator=g)).to(dt)
+        n = pkg.RMSNorm(d, eps=1e-5).to(dev, dt)
         with torch.no_grad():
             n.weight.copy_(w.to(dev))
             y = n(x.to(dev)).cpu()

@@ -98,6 +98,9 @@ SHAPES = [
     (64, 4, 1, 256, 64, 64, 64),        # r1 = 1, tiny r2
     (16, 2, 1, 128, 512, 256, 128),     # r1 = 1 on the persistent core (r1 * r2 = 512)
     (8, 2, 32, 256, 512, 768, 4608),    # the reference's default ranks (config.py:20-24)
+    (8, 2, 8, 128, 192, 256, 256),      # r1 = 8: persistent core in 2 rank groups
+    (16, 2, 12, 256, 320, 512, 256),    # r1 = 12: 3 rank groups, 5 channel tiles
+    (8, 2, 64, 64, 128, 128, 128),      # r1 = 64: 16 rank groups, r3 = 64
 ]
 
 
