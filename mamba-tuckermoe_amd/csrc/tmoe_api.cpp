@@ -76,6 +76,7 @@ hipEvent_t prof_event() {
 
 struct Layout {
   size_t z, c, idx, w, mid, raw, mpart, total;
+  int split;
 };
 
 Layout workspace_layout(const tmoe_plan* p, int64_t T) {
@@ -93,9 +94,11 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   if (T <= tmoe::kSmallT) o = align256(o + (size_t)T * (p->s.r3 + p->s.E) * sizeof(float));
   // k_core_pp in rank groups: fp32 partial sums of mid
   L.mpart = 0;
+  L.split = 1;
   if (p->core_p && tmoe::core_p_grouped(p->s.r1) && T > tmoe::kSmallT) {
+    L.split = tmoe::core_p_split(T, p->s.r1, p->s.r2);
     L.mpart = o;
-    o = align256(o + (size_t)tile_rows * p->s.r2 * sizeof(float));
+    o = align256(o + (size_t)L.split * tile_rows * p->s.r2 * sizeof(float));
   }
   L.total = o;
   return L;
@@ -372,6 +375,7 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
   a.mid = ws + L.mid;
   a.raw = reinterpret_cast<float*>(ws + L.raw);
   a.mpart = L.mpart ? reinterpret_cast<float*>(ws + L.mpart) : nullptr;
+  a.core_split = L.split;
   a.epi_mode = epi_mode;
   a.epi_a = epi_mode != TMOE_EPI_NONE ? epi_a : nullptr;
   a.epi_b = epi_mode == TMOE_EPI_RESIDUAL_SCALE ? epi_b : nullptr;

@@ -50,8 +50,9 @@ struct FwdArgs {
   void* z;                      // (T, r3)
   void* mid;                    // (T, r2)
   float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
-  float* mpart;                 // (T_pad, r2) fp32     k_core_pp with r1 > 4: partial sums
+  float* mpart;                 // (S, T_pad, r2) fp32  k_core_pp with r1 > 4: partial sums
                                 //                      over rank groups (null otherwise)
+  int core_split;               // S: parts an output tile's rank groups are split into
   // elementwise op fused into the out-projection's store (kEpi*): the FFN
   // sub-block's silu(gate) * up, or its residual + LayerScale
   int epi_mode;
@@ -74,6 +75,19 @@ constexpr int64_t kSmallT = 256;
 constexpr int kCorePRows = 256;
 constexpr int64_t kCorePScales = 4096;
 inline bool core_p_grouped(int64_t r1) { return r1 > 4; }
+// Output tiles (256 tokens x 64 channels) of the grouped core and the split S of
+// their r1 / 4 rank groups: the smallest divisor of r1 / 4 that gives at least
+// kCoreUnits work units (one per compute unit of an MI355X), at most r1 / 4.
+constexpr int64_t kCoreUnits = 256;
+inline int64_t core_p_out_tiles(int64_t T, int64_t r2) {
+  return (T + kCorePRows - 1) / kCorePRows * (r2 / 64);
+}
+inline int core_p_split(int64_t T, int64_t r1, int64_t r2) {
+  const int64_t G = r1 / 4, n = core_p_out_tiles(T, r2);
+  for (int64_t s = 1; s < G; ++s)
+    if (G % s == 0 && n * s >= kCoreUnits) return (int)s;
+  return (int)G;
+}
 inline bool core_p_supported(int64_t r1, int64_t r2, bool bf16, bool fp8w) {
   if (!bf16) return false;
   if (core_p_grouped(r1)) return r1 % 4 == 0 && r2 % 64 == 0 && !fp8w;

@@ -113,11 +113,17 @@ hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
 
 template <int R1, bool kGrouped>
 hipError_t launch_core_pp_r(const FwdArgs& a, hipStream_t st) {
-  // output tiles (each of r1 / R1 rank groups)
-  const int64_t tiles = (int64_t)cdiv(a.T, kCorePRows) * (R1 * a.r2 / 256);
+  // work units: output tiles, times the split of their rank groups when grouped
+  const int64_t tiles = (int64_t)cdiv(a.T, kCorePRows) * (R1 * a.r2 / 256) *
+                        (kGrouped ? a.core_split : 1);
   const int64_t ncu = cu_count();
   const dim3 grid((unsigned)(tiles < ncu ? tiles : ncu)), block(512);
   hipLaunchKernelGGL((dev::k_core_pp<R1, kCorePSteps, kGrouped>), grid, block, 0, st, a);
+  if (kGrouped && a.core_split > 1) {
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const int64_t n = (int64_t)cdiv(a.T, kCorePRows) * (a.r2 / 64) * 4096;   // float4s a part
+    hipLaunchKernelGGL(dev::k_core_combine, dim3(cdiv(n, 256)), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -1416,12 +1416,15 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
   const int wm = wave / TL::WN, wn = wave % TL::WN;
   const int64_t r2 = a.r2, r3 = a.r3;
   const int G = kGrouped ? (int)(a.r1 / R1) : 1;   // rank groups per output tile
+  const int S = kGrouped ? a.core_split : 1;     // parts of an output tile's rank groups
+  const int Gp = G / S;                          // rank groups per part
   const int ntn = (int)(R1 * r2 / TL::BN);       // tiles per token tile and rank group
   const int ntm = (int)((a.T + TL::BM - 1) / TL::BM);
   const int nout = ntm * ntn;                    // output tiles
+  const int nunits = nout * S;                   // work units: (output tile, part)
   const int nkt = (int)(r3 * 2 / kTileKBytes);   // K tiles per tile
-  const int my_out = ((int)blockIdx.x < nout) ? (nout - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
-  const int total = my_out * G * nkt;
+  const int my_units = ((int)blockIdx.x < nunits) ? (nunits - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = my_units * Gp * nkt;
   const int64_t row_bytes = r3 * 2;
   const int kt_rot = ((int)blockIdx.x >> 3) % nkt;
   const bool fp8 = a.core_scale_raw != nullptr;
@@ -1429,11 +1432,14 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
     for (int i = tid; i < R1 * (int)r2; i += 512) sc_lds[i] = a.core_scale_raw[i];
   }
 
-  // tile i of this work-group: output tile o = blockIdx.x + (i / G) gridDim.x (token
-  // tile tm, channel tile tn) and rank group rg = i % G
+  // tile i of this work-group: work unit u = blockIdx.x + (i / Gp) gridDim.x, i.e.
+  // output tile o = u % nout (token tile tm, channel tile tn; the parts of one
+  // output tile are nout apart, on one XCD when nout is a multiple of 8) and part
+  // u / nout, whose rank groups are rg = part Gp .. part Gp + Gp - 1
   auto coords = [&](int i, int& tm, int& tn, int& rg, int& o) __attribute__((always_inline)) {
-    o = (int)blockIdx.x + (i / G) * (int)gridDim.x;
-    rg = i % G;
+    const int u = (int)blockIdx.x + (i / Gp) * (int)gridDim.x;
+    o = u % nout;
+    rg = (u / nout) * Gp + i % Gp;
     tile_coords_of(o, ntn, nout, tm, tn);
   };
   // DMA of K tile g of this work-group's stream into `stage` (group 0's waves)
@@ -1489,11 +1495,16 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
     int tm, tn, rg, ot;
     coords(i, tm, tn, rg, ot);
     const int64_t m0 = (int64_t)tm * TL::BM;
-    // rank groups: this lane's partial sums, float4 (f, u) of wave `wave` of output tile ot
-    float4* part = G > 1 ? reinterpret_cast<float4*>(a.mpart) +
+    // rank groups: this lane's partial sums, float4 (f, u) of wave `wave` of output
+    // tile ot, one region of nout * 64 KB per part
+    const int prt = rg / Gp, gi = rg % Gp;
+    const int64_t part_floats = (int64_t)nout * 8 * FM * 4 * 64 * 4;
+    float4* part = G > 1 ? reinterpret_cast<float4*>(a.mpart + prt * part_floats) +
                                (((int64_t)ot * 8 + wave) * FM * 4) * 64 + lane
                          : nullptr;
-    const bool carry_in = G > 1 && rg > 0, carry_out = G > 1 && rg < G - 1;
+    // the part's running sum comes in from its previous group and goes out to its
+    // next group or, at its last group when S > 1, to k_core_combine
+    const bool carry_in = G > 1 && gi > 0, carry_out = G > 1 && (gi < Gp - 1 || S > 1);
 #pragma unroll
     for (int g = 0; g < QG; ++g) {
       // channel block of column blocks g * R1 .. g * R1 + R1 - 1 of this wave
@@ -1627,6 +1638,41 @@ __global__ __launch_bounds__(512) void k_core_pp(FwdArgs a) {
     }
   }
   if (grp == 0) lds_barrier();
+}
+
+// mid = sum over the S parts of k_core_pp's grouped partial sums, in part order
+// (rank groups split over S work units, so that T / 256 x r2 / 64 output tiles fill
+// the compute units). One thread per float4 of a part, in the lane-private layout
+// the core stored: output tile o, wave w (4 x 2 waves), row block f, chunk u, lane l
+// holds rows 64 (w / 2) + 32 f + (l & 31) and channels 32 qb + 8 u + 4 (l >> 5) .. + 3,
+// qb = 2 tn + w % 2, of token tile tm and channel tile tn (tile_coords_of).
+__global__ __launch_bounds__(256) void k_core_combine(FwdArgs a) {
+  const int ntn = (int)(a.r2 / 64);
+  const int ntm = (int)((a.T + kCorePRows - 1) / kCorePRows);
+  const int nout = ntm * ntn;
+  const int64_t per_part = (int64_t)nout * 8 * 2 * 4 * 64;   // float4s
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= per_part) return;
+  const int lane = (int)(i & 63), u = (int)((i >> 6) & 3), f = (int)((i >> 8) & 1),
+            w = (int)((i >> 9) & 7);
+  const int o = (int)(i >> 12);
+  int tm, tn;
+  tile_coords_of(o, ntn, nout, tm, tn);
+  const float4* src = reinterpret_cast<const float4*>(a.mpart) + i;
+  float4 t = src[0];
+  for (int p = 1; p < a.core_split; ++p) {
+    const float4 v = src[p * per_part];
+    t.x += v.x;
+    t.y += v.y;
+    t.z += v.z;
+    t.w += v.w;
+  }
+  const int64_t row = (int64_t)tm * kCorePRows + 64 * (w / 2) + 32 * f + (lane & 31);
+  const int64_t q = (int64_t)(2 * tn + w % 2) * 32 + 8 * u + 4 * (lane >> 5);
+  uint2 pk;
+  pk.x = pack_bf16x2(t.x, t.y);
+  pk.y = pack_bf16x2(t.z, t.w);
+  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.mid) + row * a.r2 + q) = pk;
 }
 
 // ---- k_outproj: out = mid U_out + bias  (model.py:101) --------------------
