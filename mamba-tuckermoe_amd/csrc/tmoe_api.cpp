@@ -76,7 +76,7 @@ hipEvent_t prof_event() {
 
 struct Layout {
   size_t z, c, idx, w, mid, raw, mpart, total;
-  int split;
+  int split, fsplit;
 };
 
 Layout workspace_layout(const tmoe_plan* p, int64_t T) {
@@ -91,7 +91,9 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
   L.mid = o; o = align256(o + (size_t)tile_rows * p->s.r2 * p->es);
   L.raw = o;
-  if (T <= tmoe::kSmallT) o = align256(o + (size_t)T * (p->s.r3 + p->s.E) * sizeof(float));
+  L.fsplit = tmoe::front_split(T, p->s.d_in, p->E_pad, p->kdtype == TMOE_BF16);
+  if (T <= tmoe::kSmallT || L.fsplit > 1)
+    o = align256(o + (size_t)L.fsplit * T * (p->s.r3 + p->s.E) * sizeof(float));
   // k_core_pp in rank groups: fp32 partial sums of mid
   L.mpart = 0;
   L.split = 1;
@@ -376,6 +378,7 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
   a.raw = reinterpret_cast<float*>(ws + L.raw);
   a.mpart = L.mpart ? reinterpret_cast<float*>(ws + L.mpart) : nullptr;
   a.core_split = L.split;
+  a.front_split = L.fsplit;
   a.epi_mode = epi_mode;
   a.epi_a = epi_mode != TMOE_EPI_NONE ? epi_a : nullptr;
   a.epi_b = epi_mode == TMOE_EPI_RESIDUAL_SCALE ? epi_b : nullptr;

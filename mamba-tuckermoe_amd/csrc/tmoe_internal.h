@@ -53,6 +53,8 @@ struct FwdArgs {
   float* mpart;                 // (S, T_pad, r2) fp32  k_core_pp with r1 > 4: partial sums
                                 //                      over rank groups (null otherwise)
   int core_split;               // S: parts an output tile's rank groups are split into
+  int front_split;              // K slices of the large-T front (raw holds that many
+                                //                      (T, r3 + E) fp32 planes), 1: none
   // elementwise op fused into the out-projection's store (kEpi*): the FFN
   // sub-block's silu(gate) * up, or its residual + LayerScale
   int epi_mode;
@@ -75,6 +77,19 @@ constexpr int64_t kSmallT = 256;
 constexpr int kCorePRows = 256;
 constexpr int64_t kCorePScales = 4096;
 inline bool core_p_grouped(int64_t r1) { return r1 > 4; }
+// K slices of the large-T bf16 front (router widths E_pad <= 128): when its
+// 64-token tiles number fewer than kCoreUnits and d_in spans at least 16 K tiles,
+// enough slices of at least 8 K tiles each to approach kCoreUnits work-groups.
+constexpr int64_t kFrontMinKTiles = 16;
+inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
+  if (!bf16 || T <= 256 || E_pad > 128) return 1;
+  const int64_t tiles = (T + 63) / 64, nkt = d_in * 2 / 128;
+  if (tiles >= 256 || nkt < kFrontMinKTiles) return 1;
+  int64_t s = (256 + tiles - 1) / tiles;
+  if (s > nkt / 8) s = nkt / 8;
+  return s > 1 ? (int)s : 1;
+}
+
 // Output tiles (256 tokens x 64 channels) of the grouped core and the split S of
 // their r1 / 4 rank groups: the smallest divisor of r1 / 4 that gives at least
 // kCoreUnits work units (one per compute unit of an MI355X), at most r1 / 4.

@@ -30,6 +30,8 @@ struct OutCfgF32 { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2, P = 
 // or, with r3 = 256, separate z and router work-groups of 32 tokens.
 // The weight rows come from L2 one DMA per K tile; a third LDS stage (when it
 // fits) issues them two tiles ahead, which hides the L2 latency.
+int cu_count();
+
 template <class Elt, int R3, int NR>
 hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
   if constexpr (R3 == 256 && NR == 8 && std::is_same<Elt, EltBF16>::value) {
@@ -42,6 +44,28 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
   constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
   constexpr int kStageBytes = (BM + R3 + 32 * NR) * 128;
   constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
+  if constexpr (BM > 32 && std::is_same<Elt, EltBF16>::value) {
+    if (a.front_split > 1) {
+      // K slices (k_front_part), then the per-token epilogue over their planes
+      const int64_t stride = a.T * (a.r3 + a.E);
+      hipLaunchKernelGGL((dev::k_front_part<Elt, R3, NR, kFrontPFA, BM, NS, WM>),
+                         dim3(cdiv(a.T, BM), a.front_split), dim3(64 * NW * WM), 0, st, a, a.raw,
+                         a.front_split);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+      hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256), 0, st, a,
+                         (const float*)a.raw, a.front_split, stride);
+      return hipGetLastError();
+    }
+    // fewer 64-token tiles than compute units: tiles of 32 tokens, twice the
+    // work-groups (each streams the weight rows once more from L2)
+    if ((int64_t)cdiv(a.T, BM) < cu_count()) {
+      constexpr int kStage32 = (32 + R3 + 32 * NR) * 128;
+      constexpr int NS32 = 3 * kStage32 <= 160 * 1024 ? 3 : 2;
+      hipLaunchKernelGGL((dev::k_front<Elt, R3, NR, kFrontPFA, 32, NS32, 1>), dim3(cdiv(a.T, 32)),
+                         dim3(64 * NW), 0, st, a);
+      return hipGetLastError();
+    }
+  }
   const dim3 grid(cdiv(a.T, BM)), block(64 * NW * WM);
   hipLaunchKernelGGL((dev::k_front<Elt, R3, NR, kFrontPFA, BM, NS, WM>), grid, block, 0, st, a);
   return hipGetLastError();
@@ -136,7 +160,7 @@ hipError_t launch_small_front_t(const FwdArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((dev::k_sk_front<Elt, MF, kSkW>), grid, block, 0, st, a, a.raw);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256), 0, st, a,
-                     (const float*)a.raw);
+                     (const float*)a.raw, 1, (int64_t)0);
   return hipGetLastError();
 }
 

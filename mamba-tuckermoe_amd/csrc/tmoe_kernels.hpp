@@ -1209,6 +1209,86 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
                                             kSmemBytes - kEpiBytes);
 }
 
+// The front in K slices, for token counts whose 64-token tiles leave most compute
+// units idle while K = d_in is long: work-group (tile, slice) computes the slice's
+// share of x [U_in | W_r^T] with k_front's main loop and writes it as fp32 to raw
+// plane `slice` (T rows of r3 + E floats); k_front_epi then adds the planes in
+// plane order and runs the per-token epilogue (RMSNorm, top-k, softmax, c).
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
+          int WMF = kFrontWM>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front_part(
+    FwdArgs a, float* __restrict__ raw, int nslices) {
+  typedef typename Elt::T T;
+  constexpr int EP = 32 * NR;
+  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
+  constexpr int NWT = NW * WMF;
+  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
+  constexpr int FM = TL::FM;
+  typedef RouterExtra<Elt, FM, NR, NW> RX;
+  constexpr int LD = EP + 1;
+  constexpr int kPlanes = RX::kSplitK ? NW : 1;
+  constexpr int kSmemBytes = cmax(TL::kLdsBytes, kPlanes * BM * LD * 4);
+  __shared__ u32x4 smem[kSmemBytes / 16];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;
+  const int64_t m0 = (int64_t)blockIdx.x * BM;
+  const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
+  const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
+  const int nkt = (int)(row_bytes / kTileKBytes);
+  const int sl = (int)blockIdx.y;
+  const int kt0 = sl * nkt / nslices, kt1 = (sl + 1) * nkt / nslices;
+  RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes + (int64_t)kt0 * kTileKBytes,
+               row_bytes, rows_valid};
+  RowLoader bl{reinterpret_cast<const char*>(a.wfront) + (int64_t)kt0 * kTileKBytes, row_bytes,
+               R3 + EP};
+  f32x16 acc[FM][TL::FN];
+  RX rx;
+  rx.init(wn, lane, BM + R3);
+  gemm_mainloop<TL, Elt>(acc, al, bl, kt1 - kt0, smem, rx);
+
+  const int W = R3 + (int)a.E;
+  float* plane = raw + (int64_t)sl * a.T * W + m0 * W;
+  // z columns straight from the accumulators: a half-wave writes 128 contiguous bytes
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < TL::FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wrow + i * 32 + acc_row(lane, e);
+        if (row < rows_valid)
+          plane[(int64_t)row * W + wn * TL::kWaveN + j * 32 + (lane & 31)] = acc[i][j][e];
+      }
+  // router columns: through LDS (split-K router: one partial plane per wave, added
+  // in wave order), the first E of them
+  __syncthreads();
+  float* lg = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < RX::RT; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wrow + i * 32 + acc_row(lane, e);
+        if constexpr (RX::kSplitK)
+          lg[(wn * BM + row) * LD + j * 32 + (lane & 31)] = rx.racc[i][j][e];
+        else
+          lg[row * LD + (wn * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
+      }
+  __syncthreads();
+  const int E = (int)a.E;
+  for (int idx = threadIdx.x; idx < BM * E; idx += TL::kThreads) {
+    const int row = idx / E, c = idx - row * E;
+    if (row < rows_valid) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kPlanes; ++w) v += lg[(w * BM + row) * LD + c];
+      plane[(int64_t)row * W + R3 + c] = v;
+    }
+  }
+}
+
 // The front for wide routers (E_pad = 32 NR > 128 with r3 = R3 = 256), in two kinds
 // of work-group over 32-token tiles: the first ceil(T / 32) compute z (x against
 // U_in^T, RMSNorm), the others the logits (x against the router rows, top-k,

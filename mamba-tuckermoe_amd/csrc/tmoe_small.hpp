@@ -200,8 +200,11 @@ __global__ __launch_bounds__(64 * W) void k_sk_front(FwdArgs a, float* raw) {
 // One wave per token: z = RMSNorm(raw z (* U_in scales)) * gain; logits; top-k
 // (rank_key order: larger first, NaN above numbers, lower index on ties);
 // softmax over the selected; c = sum_j w_j U_expert[e_j].
+// raw: nplanes planes of T rows (plane_stride floats apart), added in plane order
+// (the large-T front in K slices; the small-T front writes one plane).
 template <class Elt>
-__global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) {
+__global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, int nplanes,
+                                                   int64_t plane_stride) {
   typedef typename Elt::T T;
   // U_expert (at most 256 x 64) is staged in LDS while the rows load
   __shared__ float ue[kMaxExperts * 64];
@@ -212,6 +215,11 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) 
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= a.T) return;   // whole waves; no barriers below
   const float* row = raw + t * (R3 + E);
+  auto rawv = [&](int j) __attribute__((always_inline)) {
+    float v = row[j];
+    for (int p = 1; p < nplanes; ++p) v += row[p * plane_stride + j];
+    return v;
+  };
   float zv[4];
   float ss = 0.f;
 #pragma unroll
@@ -219,7 +227,7 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) 
     const int j = lane + 64 * q;
     float v = 0.f;
     if (j < R3) {
-      v = row[j];
+      v = rawv(j);
       if (a.zscale) v *= a.zscale[j];
     }
     zv[q] = v;
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw) 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = lane + 64 * q;
-    const float lv = e < E ? row[R3 + e] : 0.f;
+    const float lv = e < E ? rawv(R3 + e) : 0.f;
     if (a.logits && e < E) a.logits[t * E + e] = lv;
     sv[q] = mode ? capped_score(lv, a.router_scale, a.router_temperature) : lv;
     key[q] = e < E ? rank_key(sv[q], e) : 0;
