@@ -52,7 +52,8 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
                          dim3(cdiv(a.T, BM), a.front_split), dim3(64 * NW * WM), 0, st, a, a.raw,
                          a.front_split);
       if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-      hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256), 0, st, a,
+      hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256),
+                         (size_t)(a.E * a.r1) * sizeof(float), st, a,
                          (const float*)a.raw, a.front_split, stride);
       return hipGetLastError();
     }
@@ -130,6 +131,13 @@ hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
   typedef OutCfgBF16 C;
   const int64_t tiles = (int64_t)cdiv(a.T, C::BM) * cdiv(a.d_out, C::BN);
   const int64_t ncu = cu_count();
+  if (2 * tiles <= ncu) {
+    // at most half the compute units busy: tiles of 128 tokens, twice as many
+    const int64_t t128 = (int64_t)cdiv(a.T, 128) * cdiv(a.d_out, C::BN);
+    const dim3 grid((unsigned)(t128 < ncu ? t128 : ncu)), block(64 * C::WM * C::WN);
+    hipLaunchKernelGGL((dev::k_outproj_pp<128, C::BN, C::WM, C::WN>), grid, block, 0, st, a);
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)(tiles < ncu ? tiles : ncu)), block(64 * C::WM * C::WN);
   hipLaunchKernelGGL((dev::k_outproj_pp<C::BM, C::BN, C::WM, C::WN>), grid, block, 0, st, a);
   return hipGetLastError();
@@ -159,7 +167,8 @@ hipError_t launch_small_front_t(const FwdArgs& a, hipStream_t st) {
   const dim3 grid(cdiv(a.r3 + a.E, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
   hipLaunchKernelGGL((dev::k_sk_front<Elt, MF, kSkW>), grid, block, 0, st, a, a.raw);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256), 0, st, a,
+  hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256),
+                     (size_t)(a.E * a.r1) * sizeof(float), st, a,
                      (const float*)a.raw, 1, (int64_t)0);
   return hipGetLastError();
 }

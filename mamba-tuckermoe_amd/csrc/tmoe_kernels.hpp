@@ -1832,8 +1832,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
     if (a.epi_mode != kEpiNone) {
       // all 8 waves apply the epilogue in LDS (group 0 only loads); then group 1
       // stores the tile as for a plain one
-      epi_tile_in_lds<TL, 512, kOutEpiBatch>(stage, a, m0, n0, rows_valid, cols_valid,
-                                             (int)threadIdx.x);
+      constexpr int kIters = BM * BN * 2 / 16 / 512;
+      epi_tile_in_lds<TL, 512, (kIters < kOutEpiBatch ? kIters : kOutEpiBatch)>(
+          stage, a, m0, n0, rows_valid, cols_valid, (int)threadIdx.x);
       wait_vm_lds<63>();
       lds_barrier();
     }

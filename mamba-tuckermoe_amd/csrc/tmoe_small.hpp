@@ -206,8 +206,8 @@ template <class Elt>
 __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, int nplanes,
                                                    int64_t plane_stride) {
   typedef typename Elt::T T;
-  // U_expert (at most 256 x 64) is staged in LDS while the rows load
-  __shared__ float ue[kMaxExperts * 64];
+  // U_expert (E x r1 floats: the launch's dynamic LDS) is staged while the rows load
+  extern __shared__ float ue[];
   const int lane = threadIdx.x & 63;
   const int R3 = (int)a.r3, E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
   for (int i = threadIdx.x; i < E * R1; i += 256) ue[i] = a.uexp[i];
