@@ -137,14 +137,24 @@ def bench_ffn(args) -> None:
     from oracle import tucker_ffn_torch as ft
     from oracle import tucker_moe_np as onp
     n_par = min(T, 256)
+    m, x = sets[0]
     with torch.no_grad():
-        y = fused(0)
+        st = m.stages(x[:n_par])
+        got_idx = {"ffn_gate": m.ffn_gate.forward_with_routing(st["x_f"])[1],
+                   "ffn_up": m.ffn_up.forward_with_routing(st["x_f"])[1],
+                   "ffn_down": m.ffn_down.forward_with_routing(st["h"])[1]}
     torch.cuda.synchronize()
-    ref = ft.ffn_forward(x0[:n_par], params, f.k, compute_dtype=torch.float32)
-    parity = {"tokens": n_par,
-              "rel_l2_out": onp.rel_l2(y[:n_par].float().cpu().numpy(), ref.double().numpy()),
-              "reference": "oracle/tucker_ffn_torch fp32 on the bf16-valued inputs "
-                           "(rows that route differently included)"}
+    ref = ft.ffn_forward(x0[:n_par], params, f.k, compute_dtype=torch.float32, intermediates=True)
+    # rows that route alike in all three layers; the others sit on a near-tie that
+    # the bf16 rounding of a layer input moves (the GPU tests bound them)
+    same = torch.ones(n_par, dtype=torch.bool)
+    for name, gi in got_idx.items():
+        same &= (gi.cpu().sort(1).values == ref["idx"][name].sort(1).values).all(1)
+    y = st["out"].float().cpu()
+    parity = {"tokens": n_par, "rows_routed_alike": int(same.sum()),
+              "rel_l2_out": onp.rel_l2(y[same].numpy(), ref["out"][same].double().numpy()),
+              "reference": "oracle/tucker_ffn_torch fp32 on the bf16-valued inputs, over the "
+                           "rows routed alike in all three layers"}
     cpu = None
     if not args.no_cpu:
         threads = torch.get_num_threads()

@@ -759,59 +759,65 @@ __device__ __forceinline__ u32x4 epi_chunk(const FwdArgs& a, u32x4 y, int64_t ro
   return o;
 }
 
-// Applies the fused epilogue to a bf16 tile staged in LDS, in place, by NT
-// threads: each thread takes chunks tid, tid + NT, ... and loads their epi_a
-// values in batches of kBatch before combining and writing them back (one wait
-// per batch). Only loads are issued here, so a wave that never stores keeps its
-// vector-memory counter free of stores. For kEpiResScale the stage holds
-// R(gamma * y) already (stage_tile_t); out = R(x + that). For kEpiGlu out =
-// R(R(silu(g)) * y).
-template <class TL, int NT, int kBatch>
-__device__ __forceinline__ void epi_tile_in_lds(char* stage, const FwdArgs& a, int64_t m0,
-                                                int64_t n0, int rows_valid, int cols_valid,
-                                                int tid) {
-  constexpr int RB = TileStage<TL, uint16_t>::kRowBytes;
-  constexpr int CPR = TL::BN * 2 / 16;
-  constexpr int kIters = TL::BM * CPR / NT;
-  static_assert(TL::BM * CPR % NT == 0 && kIters % kBatch == 0, "whole batches");
+// The fused epilogue of a bf16 out-projection tile staged in LDS, by NT threads
+// in two steps. epi_tile_load issues the loads of this thread's epi_a chunks
+// (chunks tid, tid + NT, ...; zero past the valid rows and columns) into e, before
+// the tile is staged, so that their latency overlaps the staging; only loads are
+// issued, so a wave that never stores keeps its vector-memory counter free of
+// stores. epi_tile_apply, after the staging barrier, combines them with the
+// staged values in place: for kEpiGlu out = R(R(silu(g)) * y); for kEpiResScale
+// the stage holds R(gamma * y) already (stage_tile_t) and out = R(x + that).
+template <class TL, int NT>
+struct EpiTile {
+  static constexpr int kCPR = TL::BN * 2 / 16;
+  static constexpr int kIters = TL::BM * kCPR / NT;
+  static_assert(TL::BM * kCPR % NT == 0, "whole iterations");
+};
+template <class TL, int NT>
+__device__ __forceinline__ void epi_tile_load(u32x4* e, const FwdArgs& a, int64_t m0, int64_t n0,
+                                              int rows_valid, int cols_valid, int tid) {
+  constexpr int CPR = EpiTile<TL, NT>::kCPR;
   const uint16_t* ea = static_cast<const uint16_t*>(a.epi_a) + m0 * a.d_out + n0;
-  const bool glu = a.epi_mode == kEpiGlu;
   // opaque copy: the chunk offsets below are recomputed per tile rather than
   // hoisted out of a persistent tile loop (where they would be spilled)
   asm volatile("" : "+v"(tid));
-  for (int b = 0; b < kIters; b += kBatch) {
-    u32x4 e[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int c = tid + (b + i) * NT, row = c / CPR, ch = c - row * CPR;
-      e[i] = u32x4{0u, 0u, 0u, 0u};
-      if (row < rows_valid && ch * 8 < cols_valid)
-        e[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(ea + row * a.d_out + ch * 8));
+  for (int i = 0; i < EpiTile<TL, NT>::kIters; ++i) {
+    const int c = tid + i * NT, row = c / CPR, ch = c - row * CPR;
+    e[i] = u32x4{0u, 0u, 0u, 0u};
+    if (row < rows_valid && ch * 8 < cols_valid)
+      e[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ea + row * a.d_out + ch * 8));
+  }
+}
+template <class TL, int NT>
+__device__ __forceinline__ void epi_tile_apply(char* stage, const u32x4* e, const FwdArgs& a,
+                                               int tid) {
+  constexpr int RB = TileStage<TL, uint16_t>::kRowBytes;
+  constexpr int CPR = EpiTile<TL, NT>::kCPR;
+  const bool glu = a.epi_mode == kEpiGlu;
+  asm volatile("" : "+v"(tid));
+#pragma unroll
+  for (int i = 0; i < EpiTile<TL, NT>::kIters; ++i) {
+    const int c = tid + i * NT, row = c / CPR, ch = c - row * CPR;
+    u32x4* slot = reinterpret_cast<u32x4*>(stage + row * RB + ch * 16);
+    const u32x4 y = *slot;
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float y0 = bf16_bits_to_f32(y[j] & 0xffffu), y1 = bf16_bits_to_f32(y[j] >> 16);
+      const float e0 = bf16_bits_to_f32(e[i][j] & 0xffffu), e1 = bf16_bits_to_f32(e[i][j] >> 16);
+      o[j] = glu ? pack_bf16x2(round_as(silu_as(e0, EltBF16{}), EltBF16{}) * y0,
+                               round_as(silu_as(e1, EltBF16{}), EltBF16{}) * y1)
+                 : pack_bf16x2(e0 + y0, e1 + y1);
     }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int c = tid + (b + i) * NT, row = c / CPR, ch = c - row * CPR;
-      u32x4* slot = reinterpret_cast<u32x4*>(stage + row * RB + ch * 16);
-      const u32x4 y = *slot;
-      u32x4 o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float y0 = bf16_bits_to_f32(y[j] & 0xffffu), y1 = bf16_bits_to_f32(y[j] >> 16);
-        const float e0 = bf16_bits_to_f32(e[i][j] & 0xffffu), e1 = bf16_bits_to_f32(e[i][j] >> 16);
-        o[j] = glu ? pack_bf16x2(round_as(silu_as(e0, EltBF16{}), EltBF16{}) * y0,
-                                 round_as(silu_as(e1, EltBF16{}), EltBF16{}) * y1)
-                   : pack_bf16x2(e0 + y0, e1 + y1);
-      }
-      *slot = o;
-    }
+    *slot = o;   // rows and columns past the valid ones are never stored
   }
 }
 
 // Writes an out-projection tile staged in LDS to out (origin (m0, n0)) by the NT
 // threads t0 .. t0 + NT - 1 of the work-group (tid: this thread's index among
 // them), through the fused epilogue a.epi_mode unless kStagedFinal (the stage
-// holds the final values already, epi_tile_in_lds).
+// holds the final values already, epi_tile_apply).
 template <class TL, class T, int NT, bool kStagedFinal = false>
 __device__ __forceinline__ void flush_tile_by(const char* stage, const FwdArgs& a, int64_t m0,
                                               int64_t n0, int rows_valid, int cols_valid, int tid) {
@@ -1799,7 +1805,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj(FwdArgs a) {
 // takes tiles b, b + gridDim.x, ... Each tile is staged in LDS by all waves and
 // written out by group 1 alone, whose stores then drain during the next tile's
 // main loop (group 1 never waits on vmcnt; group 0 issues every DMA).
-constexpr int kOutEpiBatch = 12;    // epilogue chunks per thread loaded at once
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
   typedef uint16_t T;
@@ -1823,18 +1828,25 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
     RowLoader bl{reinterpret_cast<const char*>(a.uoutT) + n0 * row_bytes, row_bytes, cols_valid};
     f32x16 acc[TL::FM][TL::FN];
     gemm_mainloop_pingpong<TL, EltBF16>(acc, al, bl, (int)(row_bytes / kTileKBytes), smem);
+    // fused epilogue: all 8 waves load their share of epi_a (before the staging
+    // where the registers allow: 128-token tiles) and apply it to the staged tile
+    // after the barrier (group 0 only loads); group 1 then stores the tile as a
+    // plain one
+    constexpr bool kEarly = BM <= 128;
+    const bool epi = a.epi_mode != kEpiNone;
+    u32x4 e[EpiTile<TL, 512>::kIters];
+    if (kEarly && epi)
+      epi_tile_load<TL, 512>(e, a, m0, n0, rows_valid, cols_valid, (int)threadIdx.x);
     stage_tile_t<TL>(acc, stage, a.bias + n0, a.out_scale ? a.out_scale + n0 : nullptr,
                      cols_valid,
                      a.epi_mode == kEpiResScale ? static_cast<const uint16_t*>(a.epi_b) + n0
                                                 : nullptr);
     wait_vm_lds<63>();   // LDS writes done; stores of the previous tile may still drain
     lds_barrier();
-    if (a.epi_mode != kEpiNone) {
-      // all 8 waves apply the epilogue in LDS (group 0 only loads); then group 1
-      // stores the tile as for a plain one
-      constexpr int kIters = BM * BN * 2 / 16 / 512;
-      epi_tile_in_lds<TL, 512, (kIters < kOutEpiBatch ? kIters : kOutEpiBatch)>(
-          stage, a, m0, n0, rows_valid, cols_valid, (int)threadIdx.x);
+    if (epi) {
+      if (!kEarly)
+        epi_tile_load<TL, 512>(e, a, m0, n0, rows_valid, cols_valid, (int)threadIdx.x);
+      epi_tile_apply<TL, 512>(stage, e, a, (int)threadIdx.x);
       wait_vm_lds<63>();
       lds_barrier();
     }

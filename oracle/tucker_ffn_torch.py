@@ -52,7 +52,7 @@ def ffn_forward(x_res: torch.Tensor, params: Dict[str, torch.Tensor], top_k: int
     sub-block (norm_ffn.weight, ffn_gate.*, ffn_up.*, ffn_down.*, ls_ffn.gamma).
     Returns the new x_res (..., d) in the parameters' dtype or, with
     intermediates=True, a dict with x_f, gate, up, h (= silu(gate) * up), dn and
-    out, each (T, .). `stages` replaces the functions of STAGES by name (the
+    out, each (T, .), and idx {layer: (T, k) selected experts}. `stages` replaces the functions of STAGES by name (the
     tests' planted mistakes)."""
     st = dict(STAGES)
     if stages:
@@ -69,10 +69,15 @@ def ffn_forward(x_res: torch.Tensor, params: Dict[str, torch.Tensor], top_k: int
     gamma = params["ls_ffn.gamma"].detach().to("cpu", cd)
     x_f = rnd(st["rmsnorm"](x, g, eps))
 
+    idx = {}
+
     def layer(name, inp):
-        out = tm.forward(inp, layer_params(params, name), top_k, eps, chunk=chunk,
-                         compute_dtype=cd, router=router)
-        return rnd(out)
+        r = tm.forward(inp, layer_params(params, name), top_k, eps, chunk=chunk,
+                       compute_dtype=cd, router=router, intermediates=intermediates)
+        if not intermediates:
+            return rnd(r)
+        idx[name] = r["idx"]
+        return rnd(r["out"])
 
     gate = layer("ffn_gate", x_f)
     up = layer("ffn_up", x_f)
@@ -82,4 +87,4 @@ def ffn_forward(x_res: torch.Tensor, params: Dict[str, torch.Tensor], top_k: int
     out = out.to(dt).reshape(*batch, d)
     if not intermediates:
         return out
-    return {"x_f": x_f, "gate": gate, "up": up, "h": h, "dn": dn, "out": out}
+    return {"x_f": x_f, "gate": gate, "up": up, "h": h, "dn": dn, "out": out, "idx": idx}
