@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 3
+#define TMOE_ABI_VERSION 4
 
 /* error codes */
 #define TMOE_OK            0
@@ -95,6 +95,13 @@ void tmoe_plan_destroy(tmoe_plan* plan);
 
 /* Bytes of the packed-weight buffer for tmoe_pack_weights. */
 size_t tmoe_packed_bytes(const tmoe_plan* plan);
+
+/* Version of the packed-weight layout that tmoe_pack_weights / _fp8 write and
+ * tmoe_forward reads. No counterpart in the reference (whose checkpoints hold the
+ * module parameters, pure_torch_mlx/weights.py:74-81): a packed buffer saved to a
+ * file is valid for a library of the same layout version and plan shape; for any
+ * other, re-pack from the parameters. */
+int tmoe_packed_layout_version(void);
 
 /* Bytes of device workspace tmoe_forward needs for T tokens (T >= 0). */
 size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T);

@@ -12,13 +12,15 @@ Public surface:
   RMSNorm, LayerScale          their norm and scale modules
   synth                        seeded synthetic parameters and tokens
   fp8                          e4m3 weights with per-output-channel scales
+  checkpoint                   the reference's .npz keys (layers, FFN, out_proj) and the
+                               versioned packed file (save_packed / load_packed)
   _lib                         ctypes binding of the C ABI (include/tmoe.h)
 """
-from . import _lib, config, fp8, synth
+from . import _lib, checkpoint, config, fp8, synth
 from .config import FFN_WORKLOADS, WORKLOADS, FfnWorkload, TuckerMoEConfig, Workload
 from .module import RMSNorm, TuckerMoE, load_tucker
 from .block import LayerScale, TuckerFFN, TuckerOutProj
 
 __all__ = ["TuckerMoE", "RMSNorm", "LayerScale", "TuckerFFN", "TuckerOutProj",
            "TuckerMoEConfig", "Workload", "WORKLOADS", "FfnWorkload", "FFN_WORKLOADS", "load_tucker", "synth", "config", "fp8",
-           "_lib"]
+           "checkpoint", "_lib"]

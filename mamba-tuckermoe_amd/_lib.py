@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
@@ -30,7 +30,8 @@ STAGE_NAMES = ("front", "core", "out_proj")
 # Every function include/tmoe.h declares.
 EXPORTED = (
     "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
-    "tmoe_packed_bytes", "tmoe_workspace_bytes", "tmoe_pack_weights", "tmoe_pack_weights_fp8",
+    "tmoe_packed_bytes", "tmoe_packed_layout_version", "tmoe_workspace_bytes",
+    "tmoe_pack_weights", "tmoe_pack_weights_fp8",
     "tmoe_forward", "tmoe_forward_epi", "tmoe_rmsnorm_rows",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
@@ -85,6 +86,8 @@ def lib() -> ctypes.CDLL:
         L.tmoe_plan_destroy.argtypes = [vp]
         L.tmoe_packed_bytes.restype = sz
         L.tmoe_packed_bytes.argtypes = [vp]
+        L.tmoe_packed_layout_version.restype = ctypes.c_int
+        L.tmoe_packed_layout_version.argtypes = []
         L.tmoe_workspace_bytes.restype = sz
         L.tmoe_workspace_bytes.argtypes = [vp, i64]
         L.tmoe_pack_weights.restype = ctypes.c_int

@@ -196,6 +196,10 @@ void tmoe_plan_destroy(tmoe_plan* plan) { delete plan; }
 
 size_t tmoe_packed_bytes(const tmoe_plan* plan) { return plan ? plan->packed_bytes : 0; }
 
+// 1: front operand, gain, U_expert, core^T, U_out^T, bias, fp8 tables; 2: + P^T for
+// r1 in {1, 2, 4}; 3: P^T also for r1 = 4G in rank-group order.
+int tmoe_packed_layout_version(void) { return 3; }
+
 size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T) {
   if (!plan || T < 0) return 0;
   return workspace_layout(plan, T).total;

@@ -38,6 +38,10 @@ from . import _lib
 from . import fp8 as _fp8
 
 
+# state_dict keys of TuckerMoE's parameters, in the order of TuckerMoE._params()
+PARAM_KEYS = ("router.weight", "U_in", "inner_norm.weight", "U_expert", "core", "U_out", "bias")
+
+
 class RMSNorm(nn.Module):
     """RMSNorm (model.py:19-27): weight (dim) and eps.
 

@@ -1,0 +1,91 @@
+"""Checkpoint formats on the CPU: the reference's .npz keys (pure_torch_mlx/weights.py)
+fill the layer and sub-block modules exactly, and the packed file's metadata checks
+(format, version, layout reuse) behave. The packed buffer itself needs the GPU
+(tests/test_gpu_checkpoint.py)."""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+
+def _ref_ffn_arrays(pkg, f, pfx):
+    """A TransformerBlock's FFN under the reference checkpoint's keys (weights.py:69-72),
+    as float32 arrays like the exported .npz."""
+    p = pkg.synth.make_ffn_params(f, dtype=torch.float32)
+    names = {"ffn_gate": "ffn.gate_proj", "ffn_up": "ffn.up_proj", "ffn_down": "ffn.down_proj"}
+    out = {}
+    for k, v in p.items():
+        head, _, rest = k.partition(".")
+        key = f"{pfx}.{names[head]}.{rest}" if head in names else f"{pfx}.{k}"
+        out[key] = v.numpy()
+    return p, out
+
+
+def test_load_ffn_from_reference_keys(pkg, tmp_path):
+    f = pkg.FFN_WORKLOADS["F0"]
+    pfx = "backbone.layers.3.block"
+    p, arrays = _ref_ffn_arrays(pkg, f, pfx)
+    path = tmp_path / "ckpt.npz"
+    np.savez(path, **arrays)
+    loaded = pkg.checkpoint.load_npz(str(path))
+    m = pkg.TuckerFFN(f.d, f.cfg())
+    pkg.checkpoint.load_ffn(m, loaded, pfx)
+    sd = m.state_dict()
+    for k, v in p.items():
+        assert torch.equal(sd[k], v), k
+
+
+def test_load_out_proj_from_reference_keys(pkg):
+    w = pkg.Workload("op", 8, 128, 128, 8, 2, 4, 64, 128, torch.float32, 5)
+    lp = pkg.synth.make_params(w, affine="random")
+    pfx = "backbone.layers.0.block"
+    arrays = {f"{pfx}.out_proj.{k}": v.numpy() for k, v in lp.items()}
+    arrays[f"{pfx}.norm_out_proj.weight"] = np.full(128, 1.5, np.float32)
+    arrays[f"{pfx}.ls_out_proj.gamma"] = np.full(128, 0.25, np.float32)
+    m = pkg.TuckerOutProj(128, w.cfg())
+    pkg.checkpoint.load_out_proj(m, arrays, pfx)
+    for k, v in lp.items():
+        assert torch.equal(m.out_proj.state_dict()[k], v), k
+    assert torch.equal(m.norm_out_proj.weight.data, torch.full((128,), 1.5))
+    assert torch.equal(m.ls_out_proj.gamma.data, torch.full((128,), 0.25))
+
+
+def test_load_layer_bf16_rounds_like_reference(pkg):
+    """The reference loader converts the float32 arrays to the module dtype
+    (weights.py:11-13); load_layer does the same."""
+    w = pkg.Workload("l", 8, 64, 64, 4, 2, 2, 64, 64, torch.float32, 9)
+    lp = pkg.synth.make_params(w, affine="random")
+    arrays = {f"x.{k}": v.numpy() for k, v in lp.items()}
+    m = pkg.TuckerMoE(64, 64, w.cfg()).to(torch.bfloat16)
+    pkg.checkpoint.load_layer(m, arrays, "x")
+    for k, v in lp.items():
+        assert torch.equal(m.state_dict()[k], v.to(torch.bfloat16)), k
+
+
+def _write(path, meta, tensors=None):
+    from safetensors.torch import save_file
+    save_file(tensors or {"packed": torch.zeros(16, dtype=torch.uint8)}, str(path),
+              metadata={"tmoe": json.dumps(meta)})
+
+
+def test_packed_file_metadata_checks(pkg, tmp_path):
+    ck = pkg.checkpoint
+    good = {"format": ck.FORMAT, "format_version": ck.FORMAT_VERSION}
+    _write(tmp_path / "a.safetensors", good)
+    meta, t = ck.read_packed(str(tmp_path / "a.safetensors"))
+    assert meta == good and set(t) == {"packed"}
+    _write(tmp_path / "b.safetensors", {"format": "other"})
+    with pytest.raises(ValueError, match="not a"):
+        ck.read_packed(str(tmp_path / "b.safetensors"))
+    _write(tmp_path / "c.safetensors", dict(good, format_version=99))
+    with pytest.raises(ValueError, match="version"):
+        ck.read_packed(str(tmp_path / "c.safetensors"))
+    lv = pkg._lib.lib().tmoe_packed_layout_version()
+    assert ck.packed_reusable({"packed_layout": lv, "packed_bytes": 100}, 100)
+    assert not ck.packed_reusable({"packed_layout": lv - 1, "packed_bytes": 100}, 100)
+    assert not ck.packed_reusable({"packed_layout": lv, "packed_bytes": 99}, 100)
+
+
+def test_packed_layout_version_exported(pkg):
+    assert pkg._lib.lib().tmoe_packed_layout_version() >= 3
