@@ -78,15 +78,20 @@ constexpr int kCorePRows = 256;
 constexpr int64_t kCorePScales = 4096;
 inline bool core_p_grouped(int64_t r1) { return r1 > 4; }
 // K slices of the large-T bf16 front (router widths E_pad <= 128): when its
-// 64-token tiles number fewer than kCoreUnits and d_in spans at least 16 K tiles,
-// enough slices of at least 8 K tiles each to approach kCoreUnits work-groups.
+// 64-token tiles number at most a quarter of kCoreUnits and d_in spans at least 16
+// K tiles, enough slices (of at least 8 K tiles each, at most kMaxFrontPlanes) to
+// approach kCoreUnits work-groups.
 constexpr int64_t kFrontMinKTiles = 16;
+constexpr int kMaxFrontPlanes = 8;
 inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
   if (!bf16 || T <= 256 || E_pad > 128) return 1;
   const int64_t tiles = (T + 63) / 64, nkt = d_in * 2 / 128;
-  if (tiles >= 256 || nkt < kFrontMinKTiles) return 1;
+  // measured at d_in = 1536: slices win up to 64 tiles (T = 4096); at 128 tiles
+  // the 32-token front is faster
+  if (4 * tiles > 256 || nkt < kFrontMinKTiles) return 1;
   int64_t s = (256 + tiles - 1) / tiles;
   if (s > nkt / 8) s = nkt / 8;
+  if (s > kMaxFrontPlanes) s = kMaxFrontPlanes;
   return s > 1 ? (int)s : 1;
 }
 

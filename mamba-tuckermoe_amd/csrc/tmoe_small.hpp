@@ -200,8 +200,8 @@ __global__ __launch_bounds__(64 * W) void k_sk_front(FwdArgs a, float* raw) {
 // One wave per token: z = RMSNorm(raw z (* U_in scales)) * gain; logits; top-k
 // (rank_key order: larger first, NaN above numbers, lower index on ties);
 // softmax over the selected; c = sum_j w_j U_expert[e_j].
-// raw: nplanes planes of T rows (plane_stride floats apart), added in plane order
-// (the large-T front in K slices; the small-T front writes one plane).
+// raw: nplanes (<= kMaxFrontPlanes) planes of T rows (plane_stride floats apart),
+// added in plane order (the large-T front in K slices; the small-T front writes one).
 template <class Elt>
 __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, int nplanes,
                                                    int64_t plane_stride) {
@@ -210,16 +210,36 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
   extern __shared__ float ue[];
   const int lane = threadIdx.x & 63;
   const int R3 = (int)a.r3, E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool live = t < a.T;   // whole waves
+  // this lane's raw values (z columns lane + 64 q, logits lane + 64 q) of every
+  // plane, all loads issued before any is used and before the U_expert staging
+  // barrier; then added in plane order
+  float zr[4] = {0.f, 0.f, 0.f, 0.f}, lr[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    const float* row = raw + t * (R3 + E);
+    float zp[kMaxFrontPlanes][4], lp[kMaxFrontPlanes][4];
+#pragma unroll
+    for (int p = 0; p < kMaxFrontPlanes; ++p)
+      if (p < nplanes)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int j = lane + 64 * q;
+          zp[p][q] = j < R3 ? row[p * plane_stride + j] : 0.f;
+          lp[p][q] = j < E ? row[p * plane_stride + R3 + j] : 0.f;
+        }
+#pragma unroll
+    for (int p = 0; p < kMaxFrontPlanes; ++p)
+      if (p < nplanes)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          zr[q] += zp[p][q];
+          lr[q] += lp[p][q];
+        }
+  }
   for (int i = threadIdx.x; i < E * R1; i += 256) ue[i] = a.uexp[i];
   __syncthreads();
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= a.T) return;   // whole waves; no barriers below
-  const float* row = raw + t * (R3 + E);
-  auto rawv = [&](int j) __attribute__((always_inline)) {
-    float v = row[j];
-    for (int p = 1; p < nplanes; ++p) v += row[p * plane_stride + j];
-    return v;
-  };
+  if (!live) return;   // no barriers below
   float zv[4];
   float ss = 0.f;
 #pragma unroll
@@ -227,7 +247,7 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
     const int j = lane + 64 * q;
     float v = 0.f;
     if (j < R3) {
-      v = rawv(j);
+      v = zr[q];
       if (a.zscale) v *= a.zscale[j];
     }
     zv[q] = v;
@@ -248,7 +268,7 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = lane + 64 * q;
-    const float lv = e < E ? rawv(R3 + e) : 0.f;
+    const float lv = e < E ? lr[q] : 0.f;
     if (a.logits && e < E) a.logits[t * E + e] = lv;
     sv[q] = mode ? capped_score(lv, a.router_scale, a.router_temperature) : lv;
     key[q] = e < E ? rank_key(sv[q], e) : 0;
