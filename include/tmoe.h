@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 4
+#define TMOE_ABI_VERSION 5
 
 /* error codes */
 #define TMOE_OK            0
@@ -185,6 +185,31 @@ int tmoe_forward_epi(const tmoe_plan* plan, const void* x, int64_t T, const void
  * (model.py:337). out may not overlap x. Stream-ordered, no allocation. */
 int tmoe_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* weight, float eps,
                       int dtype, void* out, void* stream);
+
+/* The latent expert contraction of the reference's training module and its
+ * backward: FusedLatentMoE.forward / .backward (sft_cot_bundle/scripts/model.py:225-289,
+ * with the dG kernel :196-219), as called by TritonTuckerMoE.forward (:336-338).
+ *   x    x_shared     (B, r3)      dtype      out  (B, r2)  dtype
+ *   G    G_experts    (E, r3, r2)  dtype      dx   (B, r3)  dtype
+ *   idx  top_k_indices (B, k)      int64      dG   (E, r3, r2) dtype
+ *   p    top_k_probs   (B, k)      dtype      dp   (B, k)   dtype
+ *   out[b] = sum_j p[b,j] x[b] G[idx[b,j]];  with dout = dL/dout:
+ *   dx[b] = sum_j p[b,j] dout[b] G[idx[b,j]]^T,  dp[b,j] = dout[b] . (x[b] G[idx[b,j]]),
+ *   dG[e] = sum_{b,j: idx[b,j] = e} p[b,j] x[b]^T dout[b].
+ * dtype TMOE_BF16 or TMOE_F32 (products in fp32 accumulators, each output rounded
+ * once); r3 in {64, 128, 256}, r2 a multiple of 64, 1 <= k <= min(E, 16), E <= 64.
+ * An index outside [0, E) selects nothing. All pointers device, 16-byte aligned;
+ * workspace of at least tmoe_latent_workspace_bytes(...) bytes. B == 0 is a no-op.
+ * Stream-ordered, no allocation, no host synchronisation. */
+size_t tmoe_latent_workspace_bytes(int64_t B, int64_t E, int64_t r3, int64_t r2, int dtype,
+                                   int backward);
+int tmoe_latent_forward(const void* x, const void* G, const int64_t* idx, const void* p,
+                        int64_t B, int64_t E, int64_t k, int64_t r3, int64_t r2, int dtype,
+                        void* out, void* workspace, size_t workspace_bytes, void* stream);
+int tmoe_latent_backward(const void* x, const void* G, const int64_t* idx, const void* p,
+                         const void* dout, int64_t B, int64_t E, int64_t k, int64_t r3,
+                         int64_t r2, int dtype, void* dx, void* dG, void* dp, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 /* Per-stage timing, no counterpart in the reference (measurement support).
  * While enabled, every tmoe_forward records a HIP event before each of its

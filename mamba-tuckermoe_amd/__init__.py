@@ -10,6 +10,8 @@ Public surface:
   TuckerFFN, TuckerOutProj     the reference blocks' Tucker-MoE sub-blocks (block.py):
                                TransformerBlock's FFN, Mamba3Block's out_proj
   RMSNorm, LayerScale          their norm and scale modules
+  FusedLatentMoE               the training module's latent expert contraction with its
+                               backward (latent.py; autograd.Function, reference signature)
   synth                        seeded synthetic parameters and tokens
   fp8                          e4m3 weights with per-output-channel scales
   checkpoint                   the reference's .npz keys (layers, FFN, out_proj) and the
@@ -20,7 +22,9 @@ from . import _lib, checkpoint, config, fp8, synth
 from .config import FFN_WORKLOADS, WORKLOADS, FfnWorkload, TuckerMoEConfig, Workload
 from .module import RMSNorm, TuckerMoE, load_tucker
 from .block import LayerScale, TuckerFFN, TuckerOutProj
+from .latent import FusedLatentMoE, fused_latent_moe
 
 __all__ = ["TuckerMoE", "RMSNorm", "LayerScale", "TuckerFFN", "TuckerOutProj",
+           "FusedLatentMoE", "fused_latent_moe",
            "TuckerMoEConfig", "Workload", "WORKLOADS", "FfnWorkload", "FFN_WORKLOADS", "load_tucker", "synth", "config", "fp8",
            "checkpoint", "_lib"]

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
@@ -33,6 +33,7 @@ EXPORTED = (
     "tmoe_packed_bytes", "tmoe_packed_layout_version", "tmoe_workspace_bytes",
     "tmoe_pack_weights", "tmoe_pack_weights_fp8",
     "tmoe_forward", "tmoe_forward_epi", "tmoe_rmsnorm_rows",
+    "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
 
@@ -101,6 +102,14 @@ def lib() -> ctypes.CDLL:
                                        vp, vp, vp]
         L.tmoe_rmsnorm_rows.restype = ctypes.c_int
         L.tmoe_rmsnorm_rows.argtypes = [vp, i64, i64, vp, ctypes.c_float, ctypes.c_int, vp, vp]
+        L.tmoe_latent_workspace_bytes.restype = sz
+        L.tmoe_latent_workspace_bytes.argtypes = [i64, i64, i64, i64, ctypes.c_int, ctypes.c_int]
+        L.tmoe_latent_forward.restype = ctypes.c_int
+        L.tmoe_latent_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int,
+                                          vp, vp, sz, vp]
+        L.tmoe_latent_backward.restype = ctypes.c_int
+        L.tmoe_latent_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
+                                           ctypes.c_int, vp, vp, vp, vp, sz, vp]
         L.tmoe_prof_enable.restype = ctypes.c_int
         L.tmoe_prof_enable.argtypes = [ctypes.c_int]
         L.tmoe_prof_read.restype = ctypes.c_int

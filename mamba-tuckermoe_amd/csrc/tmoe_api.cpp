@@ -434,6 +434,77 @@ int tmoe_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* weight, f
   return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_rmsnorm_rows");
 }
 
+namespace {
+int latent_check(const char* who, int64_t B, int64_t E, int64_t k, int64_t r3, int64_t r2,
+                 int dtype) {
+  if (dtype != TMOE_BF16 && dtype != TMOE_F32)
+    return fail(TMOE_EINVAL, "%s: dtype %d is not TMOE_BF16 or TMOE_F32", who, dtype);
+  if (B < 0 || E < 1 || k < 1 || k > E)
+    return fail(TMOE_EINVAL, "%s: B=%lld E=%lld k=%lld", who, (long long)B, (long long)E,
+                (long long)k);
+  if (k > tmoe::kMaxTopK || E > 64)
+    return fail(TMOE_EUNSUPPORTED, "%s: at most 64 experts and top_k 16", who);
+  if ((r3 != 64 && r3 != 128 && r3 != 256) || r2 <= 0 || r2 % 64)
+    return fail(TMOE_EUNSUPPORTED, "%s: r3=%lld (64, 128 or 256), r2=%lld (a multiple of 64)",
+                who, (long long)r3, (long long)r2);
+  if (B > (int64_t)1 << 24)
+    return fail(TMOE_EUNSUPPORTED, "%s: B=%lld too large", who, (long long)B);
+  return TMOE_OK;
+}
+}  // namespace
+
+size_t tmoe_latent_workspace_bytes(int64_t B, int64_t E, int64_t r3, int64_t r2, int dtype,
+                                   int backward) {
+  if (B < 0 || E < 1 || r3 < 1 || r2 < 1 || (dtype != TMOE_BF16 && dtype != TMOE_F32)) return 0;
+  return tmoe::latent_workspace_bytes(B, E, r3, r2, dtype == TMOE_BF16 ? 2 : 4, backward != 0);
+}
+
+int tmoe_latent_forward(const void* x, const void* G, const int64_t* idx, const void* p,
+                        int64_t B, int64_t E, int64_t k, int64_t r3, int64_t r2, int dtype,
+                        void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (int rc = latent_check("tmoe_latent_forward", B, E, k, r3, r2, dtype)) return rc;
+  if (B == 0) return TMOE_OK;
+  if (!x || !G || !idx || !p || !out || !workspace)
+    return fail(TMOE_EINVAL, "tmoe_latent_forward: null pointer");
+  if (!aligned16(x) || !aligned16(G) || !aligned16(out) || !aligned16(workspace))
+    return fail(TMOE_EINVAL, "tmoe_latent_forward: x/G/out/workspace must be 16-byte aligned");
+  const size_t need = tmoe::latent_workspace_bytes(B, E, r3, r2, dtype == TMOE_BF16 ? 2 : 4, false);
+  if (workspace_bytes < need)
+    return fail(TMOE_EINVAL, "tmoe_latent_forward: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  tmoe::LatentArgs l{};
+  l.dtype = dtype; l.B = B; l.E = E; l.k = k; l.r3 = r3; l.r2 = r2;
+  l.x = x; l.G = G; l.idx = idx; l.p = p; l.out = out; l.ws = workspace;
+  const hipError_t e = tmoe::latent_forward(l, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_latent_forward");
+}
+
+int tmoe_latent_backward(const void* x, const void* G, const int64_t* idx, const void* p,
+                         const void* dout, int64_t B, int64_t E, int64_t k, int64_t r3,
+                         int64_t r2, int dtype, void* dx, void* dG, void* dp, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (int rc = latent_check("tmoe_latent_backward", B, E, k, r3, r2, dtype)) return rc;
+  if (B == 0) return TMOE_OK;
+  if (!x || !G || !idx || !p || !dout || !dx || !dG || !dp || !workspace)
+    return fail(TMOE_EINVAL, "tmoe_latent_backward: null pointer");
+  if (!aligned16(x) || !aligned16(G) || !aligned16(dout) || !aligned16(dx) || !aligned16(dG) ||
+      !aligned16(workspace))
+    return fail(TMOE_EINVAL, "tmoe_latent_backward: x/G/dout/dx/dG/workspace must be 16-byte "
+                             "aligned");
+  const size_t need = tmoe::latent_workspace_bytes(B, E, r3, r2, dtype == TMOE_BF16 ? 2 : 4, true);
+  if (workspace_bytes < need)
+    return fail(TMOE_EINVAL, "tmoe_latent_backward: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  tmoe::LatentArgs l{};
+  l.dtype = dtype; l.B = B; l.E = E; l.k = k; l.r3 = r3; l.r2 = r2;
+  l.x = x; l.G = G; l.idx = idx; l.p = p; l.dout = dout; l.dx = dx; l.dG = dG; l.dp = dp;
+  l.ws = workspace;
+  const hipError_t e = tmoe::latent_backward(l, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_latent_backward");
+}
+
 int tmoe_prof_enable(int on) {
   std::lock_guard<std::mutex> lk(g_prof.mu);
   g_prof.on = on != 0;

@@ -115,6 +115,29 @@ inline bool core_p_supported(int64_t r1, int64_t r2, bool bf16, bool fp8w) {
          (!fp8w || r1 * r2 <= kCorePScales);
 }
 
+// The latent expert contraction of the training module (tmoe_latent.hpp) and its
+// backward: x (B, r3), G (E, r3, r2), idx (B, k) int64, p (B, k), all but idx in
+// dtype; outputs out (B, r2) or dx (B, r3), dG (E, r3, r2), dp (B, k).
+struct LatentArgs {
+  int dtype;
+  int64_t B, E, k, r3, r2;
+  const void* x;
+  const void* G;
+  const int64_t* idx;
+  const void* p;
+  const void* dout;   // backward
+  void* out;          // forward
+  void* dx;
+  void* dG;
+  void* dp;
+  void* ws;
+};
+// Workspace bytes of latent_forward (backward = false) or latent_backward.
+size_t latent_workspace_bytes(int64_t B, int64_t E, int64_t r3, int64_t r2, int es,
+                              bool backward);
+hipError_t latent_forward(const LatentArgs& l, hipStream_t stream);
+hipError_t latent_backward(const LatentArgs& l, hipStream_t stream);
+
 // Each launcher enqueues one kernel on `stream` and returns hipGetLastError().
 hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);

@@ -3,6 +3,7 @@
 
 #include "tmoe_kernels.hpp"
 #include "tmoe_small.hpp"
+#include "tmoe_latent.hpp"
 
 namespace tmoe {
 namespace {
@@ -330,6 +331,156 @@ hipError_t launch_to_f32(const void* src, float* dst, int64_t n, int dtype, hipS
   else
     hipLaunchKernelGGL(dev::k_to_f32<float>, grid, block, 0, st, static_cast<const float*>(src),
                        dst, n);
+  return hipGetLastError();
+}
+
+}  // namespace tmoe
+
+// ---- latent expert contraction (training path) ------------------------------
+namespace tmoe {
+namespace {
+
+size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct LatentLayout {
+  size_t w, gt, zero, h, xt, dt, wt, parts, total;
+  int64_t bp;
+  int slices;
+};
+
+constexpr int kDgBM = 128, kDgBN = 128;
+
+LatentLayout latent_layout(int64_t B, int64_t E, int64_t r3, int64_t r2, int es, bool bwd) {
+  LatentLayout L{};
+  size_t o = 0;
+  L.w = o; o = al256(o + (size_t)B * E * 4);
+  if (!bwd) {
+    L.gt = o; o = al256(o + (size_t)r2 * E * r3 * es);
+  } else {
+    const int64_t M = E * r3;
+    L.bp = (B + 63) / 64 * 64;
+    L.zero = o; o = al256(o + (size_t)M * 4);
+    L.h = o; o = al256(o + (size_t)B * M * es);
+    L.xt = o; o = al256(o + (size_t)r3 * L.bp * es);
+    L.dt = o; o = al256(o + (size_t)r2 * L.bp * es);
+    L.wt = o; o = al256(o + (size_t)E * L.bp * 4);
+    // K slices of the dG GEMM: about 256 work-groups, each at least 4 K tiles
+    const int64_t tiles = (M + kDgBM - 1) / kDgBM * ((r2 + kDgBN - 1) / kDgBN);
+    const int64_t nkt = L.bp * es / kTileKBytes;
+    int64_t sl = (256 + tiles - 1) / tiles;
+    if (sl > nkt / 4) sl = nkt / 4;
+    L.slices = sl > 1 ? (int)sl : 1;
+    L.parts = o; o = al256(o + (size_t)L.slices * M * r2 * 4);
+  }
+  L.total = o;
+  return L;
+}
+
+template <class T>
+hipError_t transpose_pad(const void* src, void* dst, int64_t rows, int64_t cols, int64_t rows_pad,
+                         hipStream_t st) {
+  const dim3 grid(cdiv(cols, 32), cdiv(rows_pad, 32)), block(256);
+  hipLaunchKernelGGL(dev::k_transpose_pad<T>, grid, block, 0, st, static_cast<const T*>(src),
+                     static_cast<T*>(dst), rows, cols, rows_pad);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t latent_weights(const LatentArgs& l, float* w, hipStream_t st) {
+  const int64_t n = l.B * l.E;
+  hipLaunchKernelGGL(dev::k_latent_w<T>, dim3(cdiv(n, 256)), dim3(256), 0, st, l.idx,
+                     static_cast<const T*>(l.p), l.B, (int)l.k, (int)l.E, w);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t latent_workspace_bytes(int64_t B, int64_t E, int64_t r3, int64_t r2, int es, bool bwd) {
+  return latent_layout(B, E, r3, r2, es, bwd).total;
+}
+
+hipError_t latent_forward(const LatentArgs& l, hipStream_t st) {
+  const bool bf = l.dtype == kDtypeBF16;
+  const int es = bf ? 2 : 4;
+  const LatentLayout L = latent_layout(l.B, l.E, l.r3, l.r2, es, false);
+  char* ws = static_cast<char*>(l.ws);
+  float* w = reinterpret_cast<float*>(ws + L.w);
+  hipError_t e = bf ? latent_weights<uint16_t>(l, w, st) : latent_weights<float>(l, w, st);
+  if (e != hipSuccess) return e;
+  // G as (E r3, r2), transposed: the B^T operand (r2, E r3) of the Khatri-Rao GEMM
+  if ((e = launch_transpose(l.G, ws + L.gt, l.E * l.r3, l.r2, es, st)) != hipSuccess) return e;
+  FwdArgs a{};
+  a.dtype = l.dtype;
+  a.T = l.B; a.r1 = l.E; a.r3 = l.r3; a.r2 = l.r2;
+  a.z = const_cast<void*>(l.x);
+  a.c = w;
+  a.coreT = ws + L.gt;
+  a.mid = l.out;
+  return bf ? launch_core_t<EltBF16, CoreCfgBF16>(a, st) : launch_core_t<EltF32, CoreCfgF32>(a, st);
+}
+
+hipError_t latent_backward(const LatentArgs& l, hipStream_t st) {
+  const bool bf = l.dtype == kDtypeBF16;
+  const int es = bf ? 2 : 4;
+  const LatentLayout L = latent_layout(l.B, l.E, l.r3, l.r2, es, true);
+  const int64_t M = l.E * l.r3;
+  char* ws = static_cast<char*>(l.ws);
+  float* w = reinterpret_cast<float*>(ws + L.w);
+  hipError_t e = bf ? latent_weights<uint16_t>(l, w, st) : latent_weights<float>(l, w, st);
+  if (e != hipSuccess) return e;
+  // H = dout G_flat^T (B, E r3): the out-projection GEMM with U_out^T := G as (E r3, r2)
+  if ((e = launch_copy_pad(nullptr, ws + L.zero, 0, M, 4, st)) != hipSuccess) return e;
+  FwdArgs a{};
+  a.dtype = l.dtype;
+  a.T = l.B; a.r2 = l.r2; a.d_out = M;
+  a.mid = const_cast<void*>(l.dout);
+  a.uoutT = l.G;
+  a.bias = reinterpret_cast<const float*>(ws + L.zero);
+  a.out = ws + L.h;
+  if ((e = launch_outproj(a, st)) != hipSuccess) return e;
+  // dx and dp from H
+  if (bf)
+    hipLaunchKernelGGL((dev::k_latent_dx_dp<uint16_t, uint16_t>), dim3(cdiv(l.B, 4)), dim3(256), 0,
+                       st, reinterpret_cast<const uint16_t*>(ws + L.h), w,
+                       static_cast<const uint16_t*>(l.x), l.idx, l.B, (int)l.E, (int)l.k,
+                       (int)l.r3, static_cast<uint16_t*>(l.dx), static_cast<uint16_t*>(l.dp));
+  else
+    hipLaunchKernelGGL((dev::k_latent_dx_dp<float, float>), dim3(cdiv(l.B, 4)), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(ws + L.h), w, static_cast<const float*>(l.x),
+                       l.idx, l.B, (int)l.E, (int)l.k, (int)l.r3, static_cast<float*>(l.dx),
+                       static_cast<float*>(l.dp));
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  // dG: token-major transposes (zero-padded to Bp tokens), then the weighted GEMM
+  // in K slices and the sum of the slices
+  if (bf) {
+    if ((e = transpose_pad<uint16_t>(l.x, ws + L.xt, l.B, l.r3, L.bp, st)) != hipSuccess) return e;
+    if ((e = transpose_pad<uint16_t>(l.dout, ws + L.dt, l.B, l.r2, L.bp, st)) != hipSuccess) return e;
+  } else {
+    if ((e = transpose_pad<float>(l.x, ws + L.xt, l.B, l.r3, L.bp, st)) != hipSuccess) return e;
+    if ((e = transpose_pad<float>(l.dout, ws + L.dt, l.B, l.r2, L.bp, st)) != hipSuccess) return e;
+  }
+  if ((e = transpose_pad<float>(w, ws + L.wt, l.B, l.E, L.bp, st)) != hipSuccess) return e;
+  const int64_t tiles = (M + kDgBM - 1) / kDgBM * ((l.r2 + kDgBN - 1) / kDgBN);
+  float* parts = reinterpret_cast<float*>(ws + L.parts);
+  const dim3 grid((unsigned)tiles, (unsigned)L.slices), block(64 * 2 * 2);
+  if (bf)
+    hipLaunchKernelGGL((dev::k_latent_dg<EltBF16, kDgBM, kDgBN, 2, 2, 2>), grid, block, 0, st,
+                       (const void*)(ws + L.xt), reinterpret_cast<const float*>(ws + L.wt),
+                       (const void*)(ws + L.dt), L.bp, (int)l.E, (int)l.r3, (int)l.r2, L.slices,
+                       parts);
+  else
+    hipLaunchKernelGGL((dev::k_latent_dg<EltF32, kDgBM, kDgBN, 2, 2, 2>), grid, block, 0, st,
+                       (const void*)(ws + L.xt), reinterpret_cast<const float*>(ws + L.wt),
+                       (const void*)(ws + L.dt), L.bp, (int)l.E, (int)l.r3, (int)l.r2, L.slices,
+                       parts);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int64_t n = M * l.r2;
+  if (bf)
+    hipLaunchKernelGGL(dev::k_sum_planes<uint16_t>, dim3(cdiv(n, 1024) < 4096 ? cdiv(n, 1024) : 4096),
+                       dim3(256), 0, st, parts, L.slices, n, static_cast<uint16_t*>(l.dG));
+  else
+    hipLaunchKernelGGL(dev::k_sum_planes<float>, dim3(cdiv(n, 1024) < 4096 ? cdiv(n, 1024) : 4096),
+                       dim3(256), 0, st, parts, L.slices, n, static_cast<float*>(l.dG));
   return hipGetLastError();
 }
 
