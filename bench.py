@@ -185,6 +185,58 @@ def bench_ffn(args) -> None:
     }), flush=True)
 
 
+LATENT_METRIC = "FusedLatentMoE forward + backward tokens/sec (training path)"
+
+
+def bench_latent(args) -> None:
+    """--latent: one step = FusedLatentMoE forward and backward (the training
+    module's latent contraction, sft_cot_bundle/scripts/model.py:225-289) over T
+    tokens at the training config's ranks (E 8, k 2, r3 256, r2 1024), bf16."""
+    import torch
+
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    T = args.tokens or 16384
+    E, k, r3, r2 = 8, 2, 256, 1024
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(T, r3, device=dev, generator=g).bfloat16().requires_grad_(True)
+    G = (torch.randn(E, r3, r2, device=dev, generator=g) * r3 ** -0.5).bfloat16().requires_grad_(True)
+    v, idx = torch.topk(torch.randn(T, E, device=dev, generator=g), k, dim=-1)
+    p = torch.softmax(v, -1).bfloat16().requires_grad_(True)
+    dout = torch.randn(T, r2, device=dev, generator=g).bfloat16()
+
+    def step():
+        out = pkg.FusedLatentMoE.apply(x, G, idx, p)
+        out.backward(dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    algo = 8.0 * T * k * r3 * r2          # out, dx, dp, dG: 2 T k r3 r2 each
+    executed = 2.0 * T * r3 * r2 * E * 3  # dense over E: forward, H, dG
+    peak = PEAK_TFLOPS["bf16"]
+    log(f"[bench-latent] T={T}: {ms * 1e3:.1f} us per forward+backward; "
+        f"{executed / (ms * 1e-3) / 1e12:.0f} TFLOP/s executed (dense over E)")
+    print(json.dumps({
+        "metric": LATENT_METRIC, "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "FusedLatentMoE forward+backward, one GPU", "T": T, "E": E,
+                   "top_k": k, "r3": r3, "r2": r2},
+        "mfma": {"executed_tflops": executed / (ms * 1e-3) / 1e12,
+                 "algorithmic_tflops": algo / (ms * 1e-3) / 1e12, "peak": peak,
+                 "executed_frac": executed / (ms * 1e-3) / 1e12 / peak},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,6 +254,8 @@ def main():
                          "copy kernel of known size, to scale profiler byte counters)")
     ap.add_argument("--ffn", default=None,
                     help="time the FFN sub-block of this FFN workload (F0, F1, F2) instead")
+    ap.add_argument("--latent", action="store_true",
+                    help="time FusedLatentMoE forward + backward (training path) instead")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -211,6 +265,9 @@ def main():
         sys.exit(2)
     if args.ffn:
         bench_ffn(args)
+        return
+    if args.latent:
+        bench_latent(args)
         return
 
     import numpy as np

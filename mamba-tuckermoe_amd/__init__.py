@@ -12,6 +12,7 @@ Public surface:
   RMSNorm, LayerScale          their norm and scale modules
   FusedLatentMoE               the training module's latent expert contraction with its
                                backward (latent.py; autograd.Function, reference signature)
+  TuckerMoETrain               the reference's training layer (TritonTuckerMoE) on it
   synth                        seeded synthetic parameters and tokens
   fp8                          e4m3 weights with per-output-channel scales
   checkpoint                   the reference's .npz keys (layers, FFN, out_proj) and the
@@ -22,9 +23,9 @@ from . import _lib, checkpoint, config, fp8, synth
 from .config import FFN_WORKLOADS, WORKLOADS, FfnWorkload, TuckerMoEConfig, Workload
 from .module import RMSNorm, TuckerMoE, load_tucker
 from .block import LayerScale, TuckerFFN, TuckerOutProj
-from .latent import FusedLatentMoE, fused_latent_moe
+from .latent import FusedLatentMoE, TuckerMoETrain, fused_latent_moe
 
 __all__ = ["TuckerMoE", "RMSNorm", "LayerScale", "TuckerFFN", "TuckerOutProj",
-           "FusedLatentMoE", "fused_latent_moe",
+           "FusedLatentMoE", "TuckerMoETrain", "fused_latent_moe",
            "TuckerMoEConfig", "Workload", "WORKLOADS", "FfnWorkload", "FFN_WORKLOADS", "load_tucker", "synth", "config", "fp8",
            "checkpoint", "_lib"]

@@ -93,3 +93,68 @@ class FusedLatentMoE(torch.autograd.Function):
 def fused_latent_moe(x_shared, G_experts, top_k_indices, top_k_probs):
     """FusedLatentMoE.apply(...)."""
     return FusedLatentMoE.apply(x_shared, G_experts, top_k_indices, top_k_probs)
+
+
+def router_temperature(step, warmup: int = 500, total: int = 10000, t_start: float = 2.0,
+                       t_end: float = 0.5):
+    """The reference's router temperature schedule (model.py:114-120): t_end before
+    any step is given, else a cosine from t_start to t_end over steps warmup .. total."""
+    if step is None:
+        return t_end
+    s = torch.as_tensor(step, dtype=torch.float32)
+    progress = torch.clamp((s - warmup) / max(1, total - warmup), min=0.0, max=1.0)
+    return t_end + 0.5 * (t_start - t_end) * (1.0 + torch.cos(torch.pi * progress))
+
+
+def scaled_tanh(x: torch.Tensor, scale: float = 10.0) -> torch.Tensor:
+    """scale * tanh(x / scale) as 2 sigmoid(2u) - 1 (the reference's fast_scaled_tanh,
+    model.py:22-64; its backward dy (1 - t^2) is the autograd of this expression)."""
+    return scale * (2.0 * torch.sigmoid(2.0 * x / scale) - 1.0)
+
+
+class TuckerMoETrain(torch.nn.Module):
+    """The reference's training layer TritonTuckerMoE (model.py:292-340): the same
+    constructor, parameters (router.weight, U_expert, U_in, U_out, core, bias,
+    inner_norm.weight) and forward(x, step) -> (out, lb_loss, z_loss). The latent
+    expert contraction and its backward run on FusedLatentMoE (HIP); the router,
+    projections and losses are the reference's torch expressions."""
+
+    def __init__(self, dim_in, dim_out, num_experts=8, top_k=2, r1=4, r2=1024, r3=256):
+        super().__init__()
+        self.num_experts = num_experts
+        self.top_k = min(top_k, num_experts)
+        self.router = torch.nn.Linear(dim_in, num_experts, bias=False)
+        torch.nn.init.normal_(self.router.weight, mean=0.0, std=0.02)
+        self.U_expert = torch.nn.Parameter(torch.empty(num_experts, r1))
+        self.U_in = torch.nn.Parameter(torch.empty(dim_in, r3))
+        self.U_out = torch.nn.Parameter(torch.empty(r2, dim_out))
+        self.core = torch.nn.Parameter(torch.empty(r1, r3, r2))
+        self.bias = torch.nn.Parameter(torch.zeros(dim_out))
+        self.inner_norm = torch.nn.RMSNorm(r3, eps=1e-5)
+        torch.nn.init.orthogonal_(self.U_in)
+        torch.nn.init.orthogonal_(self.U_out)
+        torch.nn.init.xavier_uniform_(self.U_expert)
+        torch.nn.init.xavier_uniform_(self.core)
+
+    def forward(self, x, step=None):
+        orig = x.shape
+        xf = x.reshape(-1, orig[-1])
+        temperature = router_temperature(step)
+        raw = self.router(xf)
+        capped = scaled_tanh(raw, 10.0)
+        z_loss = torch.mean(torch.logsumexp(capped, dim=-1) ** 2) if self.training else 0.0
+        logits = capped / temperature
+        probs = torch.softmax(logits, dim=-1)
+        _, idx = torch.topk(logits, self.top_k, dim=-1)
+        top = probs.gather(-1, idx)
+        top_p = top / (top.sum(-1, keepdim=True) + 1e-6)
+        if self.training:
+            mask = torch.zeros_like(logits).scatter_(1, idx, 1.0)
+            lb_loss = self.num_experts * torch.sum(mask.mean(0) * probs.float().mean(0))
+        else:
+            lb_loss = 0.0
+        xs = self.inner_norm(torch.matmul(xf, self.U_in))
+        G = torch.einsum("er,rst->est", self.U_expert, self.core)
+        core = FusedLatentMoE.apply(xs, G, idx, top_p).to(x.dtype)
+        out = torch.matmul(core, self.U_out).reshape(*orig[:-1], -1)
+        return out + self.bias, lb_loss, z_loss

@@ -73,3 +73,40 @@ def test_latent_rejects_bad_arguments(pkg, dev):
     with pytest.raises(pkg._lib.TmoeError):
         pkg.fused_latent_moe(x[:, :48].to(dev), G[:, :48].contiguous().to(dev), idx.to(dev),
                              p.to(dev))                               # r3 = 48 unsupported
+
+
+def test_training_layer_gradients(pkg, dev):
+    """TuckerMoETrain (the reference's TritonTuckerMoE) forward and every parameter
+    gradient on the GPU against the same module on the CPU in float64 with the
+    latent contraction as a torch expression (oracle/latent_np semantics)."""
+    torch.manual_seed(0)
+    m = pkg.TuckerMoETrain(128, 96, num_experts=8, top_k=2, r1=4, r2=128, r3=64)
+    m.train()
+    x = torch.randn(3, 50, 128)
+    ref = pkg.TuckerMoETrain(128, 96, num_experts=8, top_k=2, r1=4, r2=128, r3=64).double()
+    ref.load_state_dict({k: v.double() for k, v in m.state_dict().items()})
+    ref.train()
+
+    def latent_torch(xs, G, idx, p):
+        out = 0
+        for j in range(idx.shape[1]):
+            out = out + p[:, j:j + 1] * torch.einsum("bs,bsq->bq", xs, G[idx[:, j]])
+        return out
+
+    import mamba_tuckermoe_amd.latent as lat
+    orig = lat.FusedLatentMoE.apply
+    lat.FusedLatentMoE.apply = staticmethod(latent_torch)
+    try:
+        o_ref, lb_ref, z_ref = ref(x.double(), step=700)
+        (o_ref.square().mean() + lb_ref + z_ref).backward()
+    finally:
+        lat.FusedLatentMoE.apply = orig
+    m = m.to(dev)
+    o, lb, zl = m(x.to(dev), step=700)
+    (o.square().mean() + lb + zl).backward()
+    torch.cuda.synchronize()
+    assert onp.rel_l2(o.detach().cpu().numpy(), o_ref.detach().numpy()) <= 1e-5
+    assert abs(lb.item() - lb_ref.item()) <= 1e-5 and abs(zl.item() - z_ref.item()) <= 1e-4
+    for (n, p), (_, q) in zip(m.named_parameters(), ref.named_parameters()):
+        err = onp.rel_l2(p.grad.cpu().numpy(), q.grad.numpy())
+        assert err <= 1e-4, (n, err)
