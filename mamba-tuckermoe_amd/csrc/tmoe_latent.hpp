@@ -151,7 +151,12 @@ __global__ void k_sum_planes(const float* __restrict__ parts, int nslices, int64
 }
 
 // One wave per token b: dx[b, s] = sum_e w[b, e] H[b, (e, s)] and
-// dp[b, j] = sum_s x[b, s] H[b, (idx[b, j], s)] (s in lane order, then a wave sum).
+// dp[b, j] = sum_s x[b, s] H[b, (idx[b, j], s)]. The token's H row (E r3 values) is
+// read in 16-byte chunks, kRound of a lane's chunks issued at once: with CPR = r3 / CE
+// chunks per expert (CE elements a chunk) and 64 a multiple of CPR (r3 in 64 .. 256),
+// lane l always holds column chunk l % CPR, of experts (l + 64 i) / CPR. dx adds the
+// lanes of one column chunk (a butterfly over strides CPR .. 32); dp takes each
+// selected expert's chunks and adds over the wave.
 template <class T, class P>
 __global__ __launch_bounds__(256) void k_latent_dx_dp(const T* __restrict__ H,
                                                       const float* __restrict__ w,
@@ -159,21 +164,62 @@ __global__ __launch_bounds__(256) void k_latent_dx_dp(const T* __restrict__ H,
                                                       const int64_t* __restrict__ idx, int64_t B,
                                                       int E, int k, int r3, T* __restrict__ dx,
                                                       P* __restrict__ dp) {
+  constexpr int CE = 16 / (int)sizeof(T);
+  constexpr int kRound = 8;
   const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (b >= B) return;   // whole waves
-  const T* hb = H + b * (int64_t)E * r3;
-  for (int s = lane; s < r3; s += 64) {
-    float v = 0.f;
-    for (int e = 0; e < E; ++e) v += w[b * E + e] * load_as_f32(hb + (int64_t)e * r3 + s);
-    store_from_f32(dx + b * r3 + s, v);
+  const int cpr = r3 / CE;
+  const int nch = E * cpr;                    // chunks of the row
+  const int sc = lane % cpr;                  // this lane's column chunk
+  const u32x4* hb = reinterpret_cast<const u32x4*>(H + b * (int64_t)E * r3);
+  const u32x4 xv = reinterpret_cast<const u32x4*>(x + b * r3)[sc];
+  const T* xe = reinterpret_cast<const T*>(&xv);
+  int64_t sel[kMaxTopK];
+  float dpv[kMaxTopK];
+  for (int j = 0; j < k; ++j) {
+    sel[j] = idx[b * k + j];   // outside [0, E): selects nothing, dp = 0
+    dpv[j] = 0.f;
+  }
+  float acc[CE];
+#pragma unroll
+  for (int c = 0; c < CE; ++c) acc[c] = 0.f;
+  for (int base = 0; base < nch; base += 64 * kRound) {
+    u32x4 hv[kRound];
+#pragma unroll
+    for (int i = 0; i < kRound; ++i)
+      if (base + lane + 64 * i < nch) hv[i] = hb[base + lane + 64 * i];
+#pragma unroll
+    for (int i = 0; i < kRound; ++i) {
+      const int ch = base + lane + 64 * i;
+      if (ch < nch) {
+        const int e = ch / cpr;
+        const float we = w[b * E + e];
+        const T* he = reinterpret_cast<const T*>(&hv[i]);
+        float d = 0.f;
+#pragma unroll
+        for (int c = 0; c < CE; ++c) {
+          const float hc = load_as_f32(he + c);
+          acc[c] += we * hc;
+          d += load_as_f32(xe + c) * hc;
+        }
+        for (int j = 0; j < k; ++j)
+          if (sel[j] == e) dpv[j] += d;
+      }
+    }
+  }
+  for (int off = cpr; off < 64; off <<= 1)
+#pragma unroll
+    for (int c = 0; c < CE; ++c) acc[c] += __shfl_xor(acc[c], off);
+  if (lane < cpr) {
+    u32x4 o;
+    T* oe = reinterpret_cast<T*>(&o);
+#pragma unroll
+    for (int c = 0; c < CE; ++c) store_from_f32(oe + c, acc[c]);
+    reinterpret_cast<u32x4*>(dx + b * r3)[lane] = o;
   }
   for (int j = 0; j < k; ++j) {
-    const int64_t e = idx[b * k + j];
-    float v = 0.f;
-    if (e >= 0 && e < E)   // an index outside [0, E) selects nothing: dp = 0
-      for (int s = lane; s < r3; s += 64)
-        v += load_as_f32(x + b * r3 + s) * load_as_f32(hb + e * r3 + s);
+    float v = dpv[j];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
     if (lane == 0) store_from_f32(dp + b * k + j, v);
