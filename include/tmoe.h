@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 5
+#define TMOE_ABI_VERSION 6
 
 /* error codes */
 #define TMOE_OK            0
@@ -178,6 +178,18 @@ int tmoe_forward_epi(const tmoe_plan* plan, const void* x, int64_t T, const void
                      void* out, int32_t* topk_idx, float* topk_w, float* logits,
                      void* workspace, size_t workspace_bytes, int epi_mode,
                      const void* epi_a, const void* epi_b, void* stream);
+
+/* out = R(R(silu(gate(x))) * up(x)) for two layers of one plan over the same input:
+ * F.silu(ffn_gate(x_f)) * ffn_up(x_f) of model.py:338-340, i.e. tmoe_forward of the
+ * gate's packed weights into `out` followed by tmoe_forward_epi(TMOE_EPI_GLU, out) of
+ * the up's (bit for bit the same result). The two layers' fronts run in one launch
+ * where the kernels allow (bf16, r3 = 256: the two run side by side on the compute
+ * units, which a T that leaves most of them idle per layer rewards). ws_gate and
+ * ws_up: two distinct workspaces of workspace_bytes >= tmoe_workspace_bytes(plan, T)
+ * each. No routing outputs; not recorded by tmoe_prof_*. */
+int tmoe_forward_glu(const tmoe_plan* plan, const void* x, int64_t T, const void* packed_gate,
+                     const void* packed_up, void* out, void* ws_gate, void* ws_up,
+                     size_t workspace_bytes, void* stream);
 
 /* out (T, d) = RMSNorm(x) (T, d) with gain weight (d): RMSNorm.forward of
  * model.py:25-27, (x / sqrt(mean(x^2) + eps)) * weight, computed in fp32 and

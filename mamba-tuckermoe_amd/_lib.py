@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
@@ -32,7 +32,7 @@ EXPORTED = (
     "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
     "tmoe_packed_bytes", "tmoe_packed_layout_version", "tmoe_workspace_bytes",
     "tmoe_pack_weights", "tmoe_pack_weights_fp8",
-    "tmoe_forward", "tmoe_forward_epi", "tmoe_rmsnorm_rows",
+    "tmoe_forward", "tmoe_forward_epi", "tmoe_forward_glu", "tmoe_rmsnorm_rows",
     "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
@@ -100,6 +100,8 @@ def lib() -> ctypes.CDLL:
         L.tmoe_forward_epi.restype = ctypes.c_int
         L.tmoe_forward_epi.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, ctypes.c_int,
                                        vp, vp, vp]
+        L.tmoe_forward_glu.restype = ctypes.c_int
+        L.tmoe_forward_glu.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, sz, vp]
         L.tmoe_rmsnorm_rows.restype = ctypes.c_int
         L.tmoe_rmsnorm_rows.argtypes = [vp, i64, i64, vp, ctypes.c_float, ctypes.c_int, vp, vp]
         L.tmoe_latent_workspace_bytes.restype = sz

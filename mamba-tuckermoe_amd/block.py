@@ -14,8 +14,7 @@ Both hold the reference's attribute names, so a TransformerBlock / Mamba3Block
 state_dict restricted to them loads unchanged. On the device each is a few
 launches and no elementwise pass of its own:
     norm       tmoe_rmsnorm_rows
-    gate       tmoe_forward
-    up         tmoe_forward_epi(TMOE_EPI_GLU, gate)          h = silu(gate) * up
+    gate, up   tmoe_forward_glu (the two fronts in one launch)   h = silu(gate) * up
     down       tmoe_forward_epi(TMOE_EPI_RESIDUAL_SCALE, x_res, gamma)
 Every product and elementwise op computes in fp32 and rounds to the parameter
 dtype where the reference module's op would return a tensor of that dtype.
@@ -53,6 +52,32 @@ def _check_input(x: torch.Tensor, d: int, dtype: torch.dtype, who: str) -> None:
                            f"{dtype}")
 
 
+def _same_plan(a: _lib.Plan, b: _lib.Plan) -> bool:
+    return all(getattr(a.shape, f) == getattr(b.shape, f) for f, _ in _lib.TmoeShape._fields_)
+
+
+def glu_pair(gate: TuckerMoE, up: TuckerMoE, x: torch.Tensor) -> torch.Tensor:
+    """R(R(silu(gate(x))) * up(x)) for two layers of one shape (tmoe_forward_glu: the
+    two fronts in one launch); (T, d_out). Layers whose plans differ (shape, dtype,
+    fp8 weights, router mode) take tmoe_forward then tmoe_forward_epi instead."""
+    pg, pu = gate.plan(), up.plan()
+    if not _same_plan(pg, pu):
+        g = gate(x)
+        return up.forward_raw(x, epi=_lib.TMOE_EPI_GLU, epi_a=g, out=g)[0]
+    T = x.shape[0]
+    d_out = gate.U_out.shape[1]
+    packed_g, packed_u = gate.packed(), up.packed()
+    out = torch.empty(T, d_out, dtype=x.dtype, device=x.device)
+    nws = pg.workspace_bytes(T)
+    wsg = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    wsu = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib().tmoe_forward_glu(
+            pg.ptr, x.data_ptr(), T, packed_g.data_ptr(), packed_u.data_ptr(), out.data_ptr(),
+            wsg.data_ptr(), wsu.data_ptr(), nws, torch.cuda.current_stream(x.device).cuda_stream))
+    return out
+
+
 class TuckerFFN(nn.Module):
     """TransformerBlock's FFN sub-block (model.py:292-296, :337-341)."""
 
@@ -77,8 +102,7 @@ class TuckerFFN(nn.Module):
         if not X.is_contiguous():
             X = X.contiguous()
         x_f = self.norm_ffn(X)
-        gate = self.ffn_gate(x_f)
-        h = self.ffn_up.forward_raw(x_f, epi=_lib.TMOE_EPI_GLU, epi_a=gate, out=gate)[0]
+        h = glu_pair(self.ffn_gate, self.ffn_up, x_f)
         out = X if inplace else None
         out = self.ffn_down.forward_raw(h, epi=_lib.TMOE_EPI_RESIDUAL_SCALE, epi_a=X,
                                         epi_b=self.ls_ffn.gamma, out=out)[0]

@@ -106,6 +106,48 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   return L;
 }
 
+// The kernels' arguments for one forward of plan p (epilogue fields unset).
+tmoe::FwdArgs make_args(const tmoe_plan* p, const void* x, int64_t T, const void* packed,
+                        void* out, int32_t* topk_idx, float* topk_w, float* logits,
+                        void* workspace, const Layout& L) {
+  const tmoe_shape& s = p->s;
+  const char* pk = static_cast<const char*>(packed);
+  char* ws = static_cast<char*>(workspace);
+  tmoe::FwdArgs a{};
+  a.dtype = p->kdtype;
+  a.router_mode = s.router_mode;
+  a.router_scale = s.router_scale;
+  a.router_temperature = s.router_temperature;
+  a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
+  a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
+  a.x = x;
+  a.wfront = pk + p->off_front;
+  a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
+  a.uexp = reinterpret_cast<const float*>(pk + p->off_uexp);
+  a.coreT = pk + p->off_core;
+  a.coreP = p->core_p ? pk + p->off_core_p : nullptr;
+  a.uoutT = pk + p->off_uout;
+  a.bias = reinterpret_cast<const float*>(pk + p->off_bias);
+  if (p->fp8w) {
+    a.zscale = reinterpret_cast<const float*>(pk + p->off_sin);
+    a.core_scale = reinterpret_cast<const float*>(pk + p->off_cscale);
+    a.out_scale = reinterpret_cast<const float*>(pk + p->off_sout);
+    a.core_scale_raw = reinterpret_cast<const float*>(pk + p->off_craw);
+  }
+  a.out = out;
+  a.idx = topk_idx ? topk_idx : reinterpret_cast<int32_t*>(ws + L.idx);
+  a.w = topk_w ? topk_w : reinterpret_cast<float*>(ws + L.w);
+  a.logits = logits;
+  a.c = reinterpret_cast<float*>(ws + L.c);
+  a.z = ws + L.z;
+  a.mid = ws + L.mid;
+  a.raw = reinterpret_cast<float*>(ws + L.raw);
+  a.mpart = L.mpart ? reinterpret_cast<float*>(ws + L.mpart) : nullptr;
+  a.core_split = L.split;
+  a.front_split = L.fsplit;
+  return a;
+}
+
 }  // namespace
 
 extern "C" {
@@ -347,42 +389,7 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
   if (workspace_bytes < L.total)
     return fail(TMOE_EINVAL, "tmoe_forward: workspace of %zu bytes, %zu needed for T=%lld",
                 workspace_bytes, L.total, (long long)T);
-  const tmoe_shape& s = p->s;
-  const char* pk = static_cast<const char*>(packed);
-  char* ws = static_cast<char*>(workspace);
-
-  tmoe::FwdArgs a{};
-  a.dtype = p->kdtype;
-  a.router_mode = s.router_mode;
-  a.router_scale = s.router_scale;
-  a.router_temperature = s.router_temperature;
-  a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
-  a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
-  a.x = x;
-  a.wfront = pk + p->off_front;
-  a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
-  a.uexp = reinterpret_cast<const float*>(pk + p->off_uexp);
-  a.coreT = pk + p->off_core;
-  a.coreP = p->core_p ? pk + p->off_core_p : nullptr;
-  a.uoutT = pk + p->off_uout;
-  a.bias = reinterpret_cast<const float*>(pk + p->off_bias);
-  if (p->fp8w) {
-    a.zscale = reinterpret_cast<const float*>(pk + p->off_sin);
-    a.core_scale = reinterpret_cast<const float*>(pk + p->off_cscale);
-    a.out_scale = reinterpret_cast<const float*>(pk + p->off_sout);
-    a.core_scale_raw = reinterpret_cast<const float*>(pk + p->off_craw);
-  }
-  a.out = out;
-  a.idx = topk_idx ? topk_idx : reinterpret_cast<int32_t*>(ws + L.idx);
-  a.w = topk_w ? topk_w : reinterpret_cast<float*>(ws + L.w);
-  a.logits = logits;
-  a.c = reinterpret_cast<float*>(ws + L.c);
-  a.z = ws + L.z;
-  a.mid = ws + L.mid;
-  a.raw = reinterpret_cast<float*>(ws + L.raw);
-  a.mpart = L.mpart ? reinterpret_cast<float*>(ws + L.mpart) : nullptr;
-  a.core_split = L.split;
-  a.front_split = L.fsplit;
+  tmoe::FwdArgs a = make_args(p, x, T, packed, out, topk_idx, topk_w, logits, workspace, L);
   a.epi_mode = epi_mode;
   a.epi_a = epi_mode != TMOE_EPI_NONE ? epi_a : nullptr;
   a.epi_b = epi_mode == TMOE_EPI_RESIDUAL_SCALE ? epi_b : nullptr;
@@ -416,6 +423,48 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
     ev.push_back(e);
     g_prof.pending.push_back(std::move(ev));
   }
+  return TMOE_OK;
+}
+
+int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* packed_gate,
+                     const void* packed_up, void* out, void* ws_gate, void* ws_up,
+                     size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!p) return fail(TMOE_EINVAL, "tmoe_forward_glu: null plan");
+  if (T < 0) return fail(TMOE_EINVAL, "tmoe_forward_glu: T=%lld < 0", (long long)T);
+  if (T > (int64_t)1 << 30)
+    return fail(TMOE_EUNSUPPORTED, "tmoe_forward_glu: T=%lld too large", (long long)T);
+  if (T == 0) return TMOE_OK;
+  if (!x || !packed_gate || !packed_up || !out || !ws_gate || !ws_up)
+    return fail(TMOE_EINVAL, "tmoe_forward_glu: null pointer");
+  if (!aligned16(x) || !aligned16(packed_gate) || !aligned16(packed_up) || !aligned16(out) ||
+      !aligned16(ws_gate) || !aligned16(ws_up))
+    return fail(TMOE_EINVAL, "tmoe_forward_glu: pointers must be 16-byte aligned");
+  if (ws_gate == ws_up) return fail(TMOE_EINVAL, "tmoe_forward_glu: the two workspaces coincide");
+  const Layout L = workspace_layout(p, T);
+  if (workspace_bytes < L.total)
+    return fail(TMOE_EINVAL, "tmoe_forward_glu: workspaces of %zu bytes, %zu needed for T=%lld",
+                workspace_bytes, L.total, (long long)T);
+  tmoe::FwdArgs g = make_args(p, x, T, packed_gate, out, nullptr, nullptr, nullptr, ws_gate, L);
+  tmoe::FwdArgs u = make_args(p, x, T, packed_up, out, nullptr, nullptr, nullptr, ws_up, L);
+  u.epi_mode = tmoe::kEpiGlu;   // out = silu(gate) * up, the gate output read from `out`
+  u.epi_a = out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (T <= tmoe::kSmallT) {
+    using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
+    const Launch small[kStages] = {tmoe::launch_small_front, tmoe::launch_small_core,
+                                   tmoe::launch_small_out};
+    for (const tmoe::FwdArgs* a : {&g, &u})
+      for (int i = 0; i < kStages; ++i)
+        if ((e = small[i](*a, st)) != hipSuccess) return hip_fail(e, "tmoe_forward_glu");
+    return TMOE_OK;
+  }
+  if ((e = tmoe::launch_front_pair(g, u, st)) != hipSuccess ||
+      (e = tmoe::launch_core(g, st)) != hipSuccess || (e = tmoe::launch_core(u, st)) != hipSuccess ||
+      (e = tmoe::launch_outproj(g, st)) != hipSuccess ||
+      (e = tmoe::launch_outproj(u, st)) != hipSuccess)
+    return hip_fail(e, "tmoe_forward_glu");
   return TMOE_OK;
 }
 

@@ -140,6 +140,9 @@ hipError_t latent_backward(const LatentArgs& l, hipStream_t stream);
 
 // Each launcher enqueues one kernel on `stream` and returns hipGetLastError().
 hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
+// the fronts of two layers of one shape over the same tokens, in one launch where
+// the kernels allow (bf16, r3 = 256, the plain front), else one after the other
+hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
 // small-T path: front = skinny GEMM + per-token epilogue; core; out-projection

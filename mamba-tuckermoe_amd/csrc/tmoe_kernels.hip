@@ -73,6 +73,44 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Two layers' fronts in one launch (k_front_pair) when both take the plain bf16
+// k_front path; otherwise one after the other.
+template <class Elt, int R3, int NR>
+hipError_t launch_front_pair_nr(const FwdArgs& a0, const FwdArgs& a1, hipStream_t st) {
+  if constexpr (NR < 8 && std::is_same<Elt, EltBF16>::value) {
+    if (a0.front_split == 1 && a1.front_split == 1 && a0.T == a1.T) {
+      constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
+      if ((int64_t)cdiv(a0.T, kFrontBM) < cu_count()) {
+        constexpr int kStage32 = (32 + R3 + 32 * NR) * 128;
+        constexpr int NS32 = 3 * kStage32 <= 160 * 1024 ? 3 : 2;
+        const int nt = (int)cdiv(a0.T, 32);
+        hipLaunchKernelGGL((dev::k_front_pair<Elt, R3, NR, kFrontPFA, 32, NS32, 1>),
+                           dim3(2 * nt), dim3(64 * NW), 0, st, a0, a1, nt);
+      } else {
+        constexpr int kStageBytes = (kFrontBM + R3 + 32 * NR) * 128;
+        constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
+        const int nt = (int)cdiv(a0.T, kFrontBM);
+        hipLaunchKernelGGL((dev::k_front_pair<Elt, R3, NR, kFrontPFA, kFrontBM, NS, kFrontWM>),
+                           dim3(2 * nt), dim3(64 * NW * kFrontWM), 0, st, a0, a1, nt);
+      }
+      return hipGetLastError();
+    }
+  }
+  if (hipError_t e = launch_front_nr<Elt, R3, NR>(a0, st); e != hipSuccess) return e;
+  return launch_front_nr<Elt, R3, NR>(a1, st);
+}
+
+template <class Elt, int R3>
+hipError_t launch_front_pair_r3(const FwdArgs& a0, const FwdArgs& a1, hipStream_t st) {
+  switch (a0.E_pad / 32) {
+    case 1: return launch_front_pair_nr<Elt, R3, 1>(a0, a1, st);
+    case 2: return launch_front_pair_nr<Elt, R3, 2>(a0, a1, st);
+    case 4: return launch_front_pair_nr<Elt, R3, 4>(a0, a1, st);
+    case 8: return launch_front_pair_nr<Elt, R3, 8>(a0, a1, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <class Elt, int R3>
 hipError_t launch_front_r3(const FwdArgs& a, hipStream_t st) {
   switch (a.E_pad / 32) {
@@ -214,6 +252,14 @@ struct SmallOut {
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t st) { return by_rows<SmallFront>(a, st); }
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t st) { return by_rows<SmallCore>(a, st); }
 hipError_t launch_small_out(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOut>(a, st); }
+
+hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t st) {
+  if (a0.dtype != kDtypeBF16 || a0.r3 != 256 || a0.E_pad != a1.E_pad || a0.r3 != a1.r3) {
+    if (hipError_t e = launch_front(a0, st); e != hipSuccess) return e;
+    return launch_front(a1, st);
+  }
+  return launch_front_pair_r3<EltBF16, 256>(a0, a1, st);
+}
 
 hipError_t launch_front(const FwdArgs& a, hipStream_t st) {
   return a.dtype == kDtypeBF16 ? launch_front_t<EltBF16>(a, st) : launch_front_t<EltF32>(a, st);

@@ -1159,9 +1159,9 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
   }
 }
 
-template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
-          int WMF = kFrontWM>
-__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
+// The front of token tile `tile` (rows tile * BM ..) of the layer `a`: k_front's body.
+template <class Elt, int R3, int NR, int PFA, int BM, int NS, int WMF>
+__device__ __forceinline__ void front_tile(const FwdArgs& a, int tile) {
   typedef typename Elt::T T;
   constexpr int EP = 32 * NR;
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;   // waves across the z columns
@@ -1184,7 +1184,7 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;   // column wave, first row
-  const int64_t m0 = (int64_t)blockIdx.x * BM;
+  const int64_t m0 = (int64_t)tile * BM;
   const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
   const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
   RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes, row_bytes, rows_valid};
@@ -1213,6 +1213,23 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
   front_z_epilogue<TL, Elt, R3>(acc, a, m0, rows_valid, zst, red);
   front_topk<EP, BM, TL::kThreads, kPlanes>(a, m0, rows_valid, lg, LD, red + NW * BM + BM,
                                             kSmemBytes - kEpiBytes);
+}
+
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
+          int WMF = kFrontWM>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front(FwdArgs a) {
+  front_tile<Elt, R3, NR, PFA, BM, NS, WMF>(a, (int)blockIdx.x);
+}
+
+// The fronts of two layers with one input (TransformerBlock's ffn_gate and ffn_up,
+// model.py:338-339) in one launch: work-groups 0 .. ntiles - 1 run a0's token
+// tiles, the next ntiles a1's, so the two run side by side on the compute units.
+template <class Elt, int R3, int NR, int PFA, int BM, int NS, int WMF>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front_pair(
+    FwdArgs a0, FwdArgs a1, int ntiles) {
+  const bool second = (int)blockIdx.x >= ntiles;   // uniform over the work-group
+  front_tile<Elt, R3, NR, PFA, BM, NS, WMF>(second ? a1 : a0,
+                                            (int)blockIdx.x - (second ? ntiles : 0));
 }
 
 // The front in K slices, for token counts whose 64-token tiles leave most compute

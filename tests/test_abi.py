@@ -192,3 +192,24 @@ def test_forward_epi_and_rmsnorm_validation_never_launch(pkg):
     assert rn(ok, 4, 64, ok, -1.0, lb.TMOE_BF16, ok, None) == -1
     assert rn(ok, 4, 64, None, 1e-5, lb.TMOE_BF16, ok, None) == -1
     assert rn(None, 0, 64, None, 1e-5, lb.TMOE_BF16, None, None) == 0   # T == 0: no-op
+
+
+def test_forward_glu_validation_never_launches(pkg):
+    rc, p, _ = _create(pkg)
+    L = pkg._lib.lib()
+    fg = L.tmoe_forward_glu
+    ok, ok2 = 0x10000, 0x20000
+    ws = L.tmoe_workspace_bytes(p, 64)
+    try:
+        assert fg(None, ok, 64, ok, ok, ok, ok, ok2, ws, None) == -1
+        assert fg(p, ok, -1, ok, ok, ok, ok, ok2, ws, None) == -1
+        assert fg(p, ok, 0, None, None, None, None, None, 0, None) == 0   # T == 0: no-op
+        assert fg(p, ok, 64, ok, None, ok, ok, ok2, ws, None) == -1
+        assert fg(p, ok, 64, ok, ok, ok, ok, ok, ws, None) == -1
+        assert "coincide" in L.tmoe_last_error().decode()
+        assert fg(p, ok, 64, ok, ok, ok, ok, ok2 + 8, ws, None) == -1
+        assert "aligned" in L.tmoe_last_error().decode()
+        assert fg(p, ok, 64, ok, ok, ok, ok, ok2, ws - 1, None) == -1
+        assert "workspace" in L.tmoe_last_error().decode()
+    finally:
+        L.tmoe_plan_destroy(p)

@@ -232,3 +232,27 @@ def test_outproj_subblock(pkg, dev, T):
     err = onp.rel_l2(_f64(y) - X, _f64(gamma) * ref["out"])
     assert err <= 2e-2, err
     assert onp.rel_l2(_f64(y), X + _f64(gamma) * ref["out"]) <= 1e-2
+
+
+@pytest.mark.parametrize("T", [100, 2048, 4096])
+@pytest.mark.parametrize("same_plan", [True, False])
+def test_glu_pair_equals_two_calls(pkg, dev, T, same_plan):
+    """tmoe_forward_glu (both fronts in one launch) gives, bit for bit, tmoe_forward of
+    the gate then tmoe_forward_epi(GLU) of the up; layers whose plans differ (here r1)
+    take the two-call path inside glu_pair."""
+    f = pkg.FFN_WORKLOADS["F2"]
+    wg = pkg.Workload("g", T, f.d, f.d_ff, f.E, f.k, f.r1, f.r3, f.r2, torch.bfloat16, 41)
+    wu = pkg.Workload("u", T, f.d, f.d_ff, f.E, f.k, f.r1 if same_plan else 2 * f.r1, f.r3,
+                      f.r2, torch.bfloat16, 42)
+    mods = []
+    for w in (wg, wu):
+        m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, torch.bfloat16)
+        m.load_state_dict({k: v.to(dev) for k, v in pkg.synth.make_params(w).items()})
+        mods.append(m)
+    x = pkg.synth.make_x(wg, T).to(dev)
+    with torch.no_grad():
+        h = pkg.block.glu_pair(mods[0], mods[1], x)
+        g = mods[0](x)
+        ref = mods[1].forward_raw(x, epi=pkg._lib.TMOE_EPI_GLU, epi_a=g)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(h, ref)
