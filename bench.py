@@ -129,10 +129,20 @@ def bench_ffn(args) -> None:
     ms_unfused = timed(unfused)
     tok_s = T / (ms * 1e-3)
     flops = sum(f.layer(n).flops(T)["total"] for n in ("ffn_gate", "ffn_up", "ffn_down"))
+    # what the kernels execute: the core at the plan's kernel rank (E < r1: the
+    # expert form, E of the r1 ranks' multiply-adds)
+    m0 = sets[0][0]
+    executed = 0
+    for n in ("ffn_gate", "ffn_up", "ffn_down"):
+        fl = f.layer(n).flops(T)
+        rk = getattr(m0, n).plan().core_rank()
+        executed += fl["total"] - fl["core"] + fl["core"] * rk // f.r1
     peak = PEAK_TFLOPS[dt_name]
     tflops = flops / (ms * 1e-3) / 1e12
+    tflops_exec = executed / (ms * 1e-3) / 1e12
     log(f"[bench-ffn] fused {ms * 1e3:.1f} us/step ({tok_s / 1e6:.2f} M tok/s, {tflops:.0f} "
-        f"TFLOP/s); separate elementwise kernels {ms_unfused * 1e3:.1f} us/step")
+        f"TFLOP/s of the reference form, {tflops_exec:.0f} executed); separate elementwise "
+        f"kernels {ms_unfused * 1e3:.1f} us/step")
 
     from oracle import tucker_ffn_torch as ft
     from oracle import tucker_moe_np as onp
@@ -179,7 +189,9 @@ def bench_ffn(args) -> None:
         "config": {"workload": f"{f.name}: TransformerBlock FFN sub-block, one GPU", "T": T,
                    "d": f.d, "d_ff": f.d_ff, "E": f.E, "top_k": f.k, "r1": f.r1, "r3": f.r3,
                    "r2": f.r2, "rotated_sets": n_sets},
-        "mfma": {"tflops": tflops, "peak": peak, "frac": tflops / peak, "flops_per_step": flops},
+        "mfma": {"tflops": tflops, "peak": peak, "frac": tflops / peak, "flops_per_step": flops,
+                 "executed_tflops": tflops_exec, "executed_frac": tflops_exec / peak,
+                 "executed_flops_per_step": executed},
         "separate_elementwise_ms_per_step": ms_unfused,
         "parity": parity, "cpu_baseline": cpu,
     }), flush=True)

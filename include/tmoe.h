@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 6
+#define TMOE_ABI_VERSION 7
 
 /* error codes */
 #define TMOE_OK            0
@@ -95,6 +95,16 @@ void tmoe_plan_destroy(tmoe_plan* plan);
 
 /* Bytes of the packed-weight buffer for tmoe_pack_weights. */
 size_t tmoe_packed_bytes(const tmoe_plan* plan);
+
+/* Rank of the core contraction the kernels run for this plan (0 for a null plan):
+ * r1, or E when the plan has fewer experts than ranks and its weights are not fp8
+ * (and the persistent core kernel is kept). Then tmoe_pack_weights packs the
+ * expert form of model.py:87-98, G_e = sum_r U_expert[e, r] core[r] (E x r3 x r2,
+ * summed in fp32 and rounded once to the weight dtype, as the reference's per-slot
+ * einsum rounds its product), with U_expert the identity: the same layer with E/r1
+ * of the core's multiply-adds. No counterpart in the reference (its module always
+ * forms the per-token expert matrices). */
+int64_t tmoe_plan_core_rank(const tmoe_plan* plan);
 
 /* Version of the packed-weight layout that tmoe_pack_weights / _fp8 write and
  * tmoe_forward reads. No counterpart in the reference (whose checkpoints hold the

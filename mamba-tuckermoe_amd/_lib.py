@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
@@ -31,6 +31,7 @@ STAGE_NAMES = ("front", "core", "out_proj")
 EXPORTED = (
     "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
     "tmoe_packed_bytes", "tmoe_packed_layout_version", "tmoe_workspace_bytes",
+    "tmoe_plan_core_rank",
     "tmoe_pack_weights", "tmoe_pack_weights_fp8",
     "tmoe_forward", "tmoe_forward_epi", "tmoe_forward_glu", "tmoe_rmsnorm_rows",
     "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
@@ -87,6 +88,8 @@ def lib() -> ctypes.CDLL:
         L.tmoe_plan_destroy.argtypes = [vp]
         L.tmoe_packed_bytes.restype = sz
         L.tmoe_packed_bytes.argtypes = [vp]
+        L.tmoe_plan_core_rank.restype = ctypes.c_int64
+        L.tmoe_plan_core_rank.argtypes = [vp]
         L.tmoe_packed_layout_version.restype = ctypes.c_int
         L.tmoe_packed_layout_version.argtypes = []
         L.tmoe_workspace_bytes.restype = sz
@@ -176,6 +179,10 @@ class Plan:
 
     def workspace_bytes(self, T: int) -> int:
         return int(lib().tmoe_workspace_bytes(self._ptr, T))
+
+    def core_rank(self) -> int:
+        """Rank of the core contraction the kernels run (r1, or E in the expert form)."""
+        return int(lib().tmoe_plan_core_rank(self._ptr))
 
     def __del__(self):
         ptr, self._ptr = getattr(self, "_ptr", None), None

@@ -30,6 +30,10 @@ struct tmoe_plan {
   size_t off_sin, off_cscale, off_sout, off_craw, packed_bytes;
   bool core_p;      // the core runs k_core_pp (T > kSmallT) from P^T at off_core_p
   size_t off_core_p;
+  // rank of the contraction the kernels run: r1, or E for plans packed in the
+  // expert form (fewer experts than ranks, weights not fp8): U_expert packed as
+  // the identity (E x E) and core as G_e = sum_r U_expert[e, r] core_r
+  int64_t rk;
 };
 
 namespace {
@@ -86,7 +90,7 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   const int64_t tile_rows =
       p->core_p ? (T + tmoe::kCorePRows - 1) / tmoe::kCorePRows * tmoe::kCorePRows : T;
   L.z = o;   o = align256(o + (size_t)T * p->s.r3 * p->es);
-  L.c = o;   o = align256(o + (size_t)tile_rows * p->s.r1 * sizeof(float));
+  L.c = o;   o = align256(o + (size_t)tile_rows * p->rk * sizeof(float));
   L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
   L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
   L.mid = o; o = align256(o + (size_t)tile_rows * p->s.r2 * p->es);
@@ -97,8 +101,8 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   // k_core_pp in rank groups: fp32 partial sums of mid
   L.mpart = 0;
   L.split = 1;
-  if (p->core_p && tmoe::core_p_grouped(p->s.r1) && T > tmoe::kSmallT) {
-    L.split = tmoe::core_p_split(T, p->s.r1, p->s.r2);
+  if (p->core_p && tmoe::core_p_grouped(p->rk) && T > tmoe::kSmallT) {
+    L.split = tmoe::core_p_split(T, p->rk, p->s.r2);
     L.mpart = o;
     o = align256(o + (size_t)L.split * tile_rows * p->s.r2 * sizeof(float));
   }
@@ -119,7 +123,7 @@ tmoe::FwdArgs make_args(const tmoe_plan* p, const void* x, int64_t T, const void
   a.router_scale = s.router_scale;
   a.router_temperature = s.router_temperature;
   a.T = T; a.d_in = s.d_in; a.d_out = s.d_out; a.E = s.E; a.E_pad = p->E_pad; a.k = s.k;
-  a.r1 = s.r1; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
+  a.r1 = p->rk; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
   a.x = x;
   a.wfront = pk + p->off_front;
   a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
@@ -215,8 +219,14 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   p->off_router = o + (size_t)s.r3 * s.d_in * p->es;
   o = align256(p->off_router + (size_t)p->E_pad * s.d_in * p->es);
   p->off_gain = o; o = align256(o + (size_t)s.r3 * sizeof(float));
-  p->off_uexp = o; o = align256(o + (size_t)s.E * s.r1 * sizeof(float));
-  p->off_core = o; o = align256(o + (size_t)s.r2 * s.r1 * s.r3 * p->es);
+  // the expert form when it contracts fewer ranks and keeps the persistent core
+  const bool bf = p->kdtype == TMOE_BF16;
+  p->rk = s.r1;
+  if (!p->fp8w && s.E < s.r1 &&
+      (tmoe::core_p_supported(s.E, s.r2, bf, false) || !tmoe::core_p_supported(s.r1, s.r2, bf, false)))
+    p->rk = s.E;
+  p->off_uexp = o; o = align256(o + (size_t)s.E * p->rk * sizeof(float));
+  p->off_core = o; o = align256(o + (size_t)s.r2 * p->rk * s.r3 * p->es);
   p->off_uout = o; o = align256(o + (size_t)s.d_out * s.r2 * p->es);
   p->off_bias = o; o = align256(o + (size_t)s.d_out * sizeof(float));
   p->off_sin = p->off_cscale = p->off_sout = p->off_craw = 0;
@@ -226,9 +236,9 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     p->off_sout = o;   o = align256(o + (size_t)s.d_out * sizeof(float));
     p->off_craw = o;   o = align256(o + (size_t)s.r1 * s.r2 * sizeof(float));
   }
-  p->core_p = tmoe::core_p_supported(s.r1, s.r2, p->kdtype == TMOE_BF16, p->fp8w);
+  p->core_p = tmoe::core_p_supported(p->rk, s.r2, bf, p->fp8w);
   p->off_core_p = 0;
-  if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)s.r1 * s.r2 * s.r3 * p->es); }
+  if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)p->rk * s.r2 * s.r3 * p->es); }
   p->packed_bytes = o;
   *plan_out = p;
   return TMOE_OK;
@@ -238,9 +248,12 @@ void tmoe_plan_destroy(tmoe_plan* plan) { delete plan; }
 
 size_t tmoe_packed_bytes(const tmoe_plan* plan) { return plan ? plan->packed_bytes : 0; }
 
+int64_t tmoe_plan_core_rank(const tmoe_plan* plan) { return plan ? plan->rk : 0; }
+
 // 1: front operand, gain, U_expert, core^T, U_out^T, bias, fp8 tables; 2: + P^T for
-// r1 in {1, 2, 4}; 3: P^T also for r1 = 4G in rank-group order.
-int tmoe_packed_layout_version(void) { return 3; }
+// r1 in {1, 2, 4}; 3: P^T also for r1 = 4G in rank-group order; 4: plans with fewer
+// experts than ranks packed in the expert form (identity U_expert, core G).
+int tmoe_packed_layout_version(void) { return 4; }
 
 size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T) {
   if (!plan || T < 0) return 0;
@@ -276,17 +289,32 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
   if ((e = tmoe::launch_to_f32(inner_w, reinterpret_cast<float*>(base + p->off_gain), s.r3,
                                s.dtype, st)) != hipSuccess)
     return hip_fail(e, "pack inner_norm.weight");
-  if ((e = tmoe::launch_to_f32(U_expert, reinterpret_cast<float*>(base + p->off_uexp),
-                               s.E * s.r1, s.dtype, st)) != hipSuccess)
-    return hip_fail(e, "pack U_expert");
-  if ((e = tmoe::launch_transpose(core, base + p->off_core, s.r1 * s.r3, s.r2, es, st)) !=
-      hipSuccess)
-    return hip_fail(e, "pack core");
-  if (p->core_p &&
-      (e = tmoe::launch_pack_core_p(core, false, nullptr,
-                                    reinterpret_cast<uint16_t*>(base + p->off_core_p), s.r1, s.r3,
-                                    s.r2, st)) != hipSuccess)
-    return hip_fail(e, "pack core (P layout)");
+  if (p->rk != s.r1) {
+    // expert form: core^T of G, P^T from it, U_expert the identity
+    if ((e = tmoe::launch_eye(reinterpret_cast<float*>(base + p->off_uexp), s.E, st)) !=
+        hipSuccess)
+      return hip_fail(e, "pack U_expert (identity)");
+    if ((e = tmoe::launch_mix_core_t(U_expert, core, base + p->off_core, s.E, s.r1, s.r3, s.r2,
+                                     es, st)) != hipSuccess)
+      return hip_fail(e, "pack core (expert form)");
+    if (p->core_p &&
+        (e = tmoe::launch_pack_core_p(base + p->off_core, false, nullptr,
+                                      reinterpret_cast<uint16_t*>(base + p->off_core_p), p->rk,
+                                      s.r3, s.r2, st, true)) != hipSuccess)
+      return hip_fail(e, "pack core (P layout)");
+  } else {
+    if ((e = tmoe::launch_to_f32(U_expert, reinterpret_cast<float*>(base + p->off_uexp),
+                                 s.E * s.r1, s.dtype, st)) != hipSuccess)
+      return hip_fail(e, "pack U_expert");
+    if ((e = tmoe::launch_transpose(core, base + p->off_core, s.r1 * s.r3, s.r2, es, st)) !=
+        hipSuccess)
+      return hip_fail(e, "pack core");
+    if (p->core_p &&
+        (e = tmoe::launch_pack_core_p(core, false, nullptr,
+                                      reinterpret_cast<uint16_t*>(base + p->off_core_p), s.r1,
+                                      s.r3, s.r2, st)) != hipSuccess)
+      return hip_fail(e, "pack core (P layout)");
+  }
   if ((e = tmoe::launch_transpose(U_out, base + p->off_uout, s.r2, s.d_out, es, st)) !=
       hipSuccess)
     return hip_fail(e, "pack U_out");

@@ -155,10 +155,18 @@ hipError_t launch_small_out(const FwdArgs& a, hipStream_t stream);
 // scale colscale[(row / group) * cols + col] is zero are stored as zero.
 hipError_t launch_transpose_e4m3(const uint8_t* src, uint16_t* dst, int64_t rows, int64_t cols,
                                  const float* colscale, int64_t group, hipStream_t stream);
-// k_core_pp's P^T (r1*r2, r3) from core (r1, r3, r2): bf16 bits, or e4m3 codes with
-// channel scales sc (r1, r2) (null for bf16; a zero scale packs its channel as zeros).
+// k_core_pp's P^T (r1*r2, r3) from core (r1, r3, r2), or with src_t from core^T
+// (r2, r1*r3): bf16 bits, or e4m3 codes with channel scales sc (r1, r2) (null for
+// bf16; a zero scale packs its channel as zeros).
 hipError_t launch_pack_core_p(const void* core, bool e4m3, const float* sc, uint16_t* dst,
-                              int64_t r1, int64_t r3, int64_t r2, hipStream_t stream);
+                              int64_t r1, int64_t r3, int64_t r2, hipStream_t stream,
+                              bool src_t = false);
+// core^T (r2, E*r3) of the expert form G_e = sum_r U_expert[e, r] core_r from
+// U_expert (E, r1) and core (r1, r3, r2), element size es (2: bf16, 4: fp32).
+hipError_t launch_mix_core_t(const void* uexp, const void* core, void* dst, int64_t E, int64_t r1,
+                             int64_t r3, int64_t r2, int es, hipStream_t stream);
+// dst (n, n) fp32 = identity
+hipError_t launch_eye(float* dst, int64_t n, hipStream_t stream);
 // core scale table (r1, r2) from the per-channel scales sc (r1, r2)
 hipError_t launch_core_scales(const float* sc, float* cs, int64_t r1, int64_t r2,
                               hipStream_t stream);

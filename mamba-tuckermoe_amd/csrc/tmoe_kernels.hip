@@ -281,13 +281,38 @@ hipError_t launch_core(const FwdArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_pack_core_p(const void* core, bool e4m3, const float* sc, uint16_t* dst,
-                              int64_t r1, int64_t r3, int64_t r2, hipStream_t st) {
+                              int64_t r1, int64_t r3, int64_t r2, hipStream_t st, bool src_t) {
   if (r1 == 0 || r2 == 0 || r3 == 0) return hipSuccess;
   const dim3 grid(cdiv(r2, 32), cdiv(r3, 32), (unsigned)r1), block(256);
   if (e4m3)
-    hipLaunchKernelGGL(dev::k_pack_core_p<true>, grid, block, 0, st, core, dst, r1, r3, r2, sc);
+    hipLaunchKernelGGL(dev::k_pack_core_p<true>, grid, block, 0, st, core, dst, r1, r3, r2, sc,
+                       src_t);
   else
-    hipLaunchKernelGGL(dev::k_pack_core_p<false>, grid, block, 0, st, core, dst, r1, r3, r2, sc);
+    hipLaunchKernelGGL(dev::k_pack_core_p<false>, grid, block, 0, st, core, dst, r1, r3, r2, sc,
+                       src_t);
+  return hipGetLastError();
+}
+
+hipError_t launch_mix_core_t(const void* uexp, const void* core, void* dst, int64_t E, int64_t r1,
+                             int64_t r3, int64_t r2, int es, hipStream_t st) {
+  if (E == 0 || r2 == 0 || r3 == 0) return hipSuccess;
+  if (r1 > 64 || r3 % 32 || r2 % 32) return hipErrorInvalidValue;
+  const dim3 grid(cdiv(r2, 32), cdiv(E * r3, 32)), block(256);
+  if (es == 2)
+    hipLaunchKernelGGL(dev::k_mix_core_t<uint16_t>, grid, block, 0, st,
+                       static_cast<const uint16_t*>(uexp), static_cast<const uint16_t*>(core),
+                       static_cast<uint16_t*>(dst), E, r1, r3, r2);
+  else
+    hipLaunchKernelGGL(dev::k_mix_core_t<float>, grid, block, 0, st,
+                       static_cast<const float*>(uexp), static_cast<const float*>(core),
+                       static_cast<float*>(dst), E, r1, r3, r2);
+  return hipGetLastError();
+}
+
+hipError_t launch_eye(float* dst, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const dim3 grid(cdiv(n * n, 256) < 1024 ? cdiv(n * n, 256) : 1024), block(256);
+  hipLaunchKernelGGL(dev::k_eye, grid, block, 0, st, dst, n);
   return hipGetLastError();
 }
 

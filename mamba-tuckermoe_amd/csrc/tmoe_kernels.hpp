@@ -1893,6 +1893,40 @@ __global__ void k_transpose(const T* __restrict__ src, T* __restrict__ dst, int6
   }
 }
 
+// The expert form of the core for plans with fewer experts than ranks:
+// mid = sum_r c_r z core_r with c = sum_j w_j U_expert[e_j] equals
+// sum_j w_j z G_{e_j} with G_e = sum_r U_expert[e, r] core_r (E x r3 x r2), a
+// contraction over E instead of r1 ranks. Each element is summed over r in rank
+// order in fp32 and rounded once to T, and written transposed as the core^T
+// operand: dst[q][e r3 + s] = G[e][s][q] (r2 rows of E r3). 32 x 32 tiles of
+// (e r3 + s, q): r3 and r2 are multiples of 32, so a tile lies in one e; r1 <= 64.
+template <class T>
+__global__ void k_mix_core_t(const T* __restrict__ uexp, const T* __restrict__ core,
+                             T* __restrict__ dst, int64_t E, int64_t r1, int64_t r3, int64_t r2) {
+  __shared__ float ue[64];
+  __shared__ float tile[32][33];
+  const int64_t q0 = (int64_t)blockIdx.x * 32, row0 = (int64_t)blockIdx.y * 32;
+  const int64_t e = row0 / r3, s0 = row0 - e * r3;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8 threads
+  if (threadIdx.x < r1) ue[threadIdx.x] = load_as_f32(uexp + e * r1 + threadIdx.x);
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) {
+    float v = 0.f;
+    for (int64_t r = 0; r < r1; ++r)
+      v = fmaf(ue[r], load_as_f32(core + (r * r3 + s0 + y) * r2 + q0 + tx), v);
+    tile[y][tx] = v;
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) store_from_f32(dst + (q0 + y) * (E * r3) + row0 + tx, tile[tx][y]);
+}
+
+// dst (n x n floats) = the identity: U_expert of a plan packed in the expert form.
+__global__ void k_eye(float* __restrict__ dst, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n * n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = i / n == i % n ? 1.f : 0.f;
+}
+
 // OCP e4m3 (1-4-3, bias 7, no infinities, S.1111.111 = NaN) to bf16 bits. Every
 // e4m3 value is exactly representable in bf16.
 __device__ __forceinline__ uint16_t e4m3_to_bf16_bits(uint32_t b) {
@@ -1936,14 +1970,17 @@ __global__ void k_transpose_e4m3(const uint8_t* __restrict__ src, uint16_t* __re
 // bf16 bits (codes == false) or e4m3 codes with per-channel scales sc (r1, r2), a
 // channel whose scale is zero packed as zeros. One work-group per (channel block
 // qb, 32 columns s, rank r).
+// src_t: the source is core^T (r2, r1 r3) instead of core (r1, r3, r2).
 template <bool kE4M3>
 __global__ void k_pack_core_p(const void* __restrict__ src, uint16_t* __restrict__ dst,
-                              int64_t r1, int64_t r3, int64_t r2, const float* __restrict__ sc) {
+                              int64_t r1, int64_t r3, int64_t r2, const float* __restrict__ sc,
+                              bool src_t) {
   __shared__ uint16_t t[32][33];
   const int64_t qb = blockIdx.x, s0 = (int64_t)blockIdx.y * 32, r = blockIdx.z;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8 threads
   for (int y = ty; y < 32; y += 8) {
-    const int64_t i = (r * r3 + s0 + y) * r2 + qb * 32 + tx;
+    const int64_t i = src_t ? (qb * 32 + tx) * (r1 * r3) + r * r3 + s0 + y
+                            : (r * r3 + s0 + y) * r2 + qb * 32 + tx;
     uint16_t v;
     if constexpr (kE4M3) {
       v = e4m3_to_bf16_bits(static_cast<const uint8_t*>(src)[i]);

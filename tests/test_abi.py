@@ -213,3 +213,25 @@ def test_forward_glu_validation_never_launches(pkg):
         assert "workspace" in L.tmoe_last_error().decode()
     finally:
         L.tmoe_plan_destroy(p)
+
+
+@pytest.mark.parametrize("kw,rank", [
+    (dict(E=16, r1=4, dtype=1), 4),                # the north-star shape: r1 form
+    (dict(E=8, r1=32, r2=512, r3=256, dtype=1), 8),   # reference ranks: expert form
+    (dict(E=8, r1=32, r2=512, r3=256, dtype=0), 8),   # fp32: expert form (k_core)
+    (dict(E=3, k=2, r1=8, dtype=1), 8),            # bf16: E = 3 would leave the persistent core
+    (dict(E=3, k=2, r1=8, dtype=0), 3),
+    (dict(E=1, k=1, r1=4, dtype=1), 1),
+    (dict(E=8, r1=32, r2=512, r3=256, dtype=2), 32),  # fp8 weights: never re-formed
+])
+def test_plan_core_rank(pkg, kw, rank):
+    """tmoe_plan_core_rank: E for plans with fewer experts than ranks (not fp8, and
+    not trading the persistent core for the Khatri-Rao one), else r1."""
+    rc, p, err = _create(pkg, **kw)
+    assert rc == 0, err
+    L = pkg._lib.lib()
+    try:
+        assert L.tmoe_plan_core_rank(p) == rank
+    finally:
+        L.tmoe_plan_destroy(p)
+    assert L.tmoe_plan_core_rank(None) == 0

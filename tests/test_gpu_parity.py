@@ -100,7 +100,10 @@ SHAPES = [
     (8, 2, 32, 256, 512, 768, 4608),    # the reference's default ranks (config.py:20-24)
     (8, 2, 8, 128, 192, 256, 256),      # r1 = 8: persistent core in 2 rank groups
     (16, 2, 12, 256, 320, 512, 256),    # r1 = 12: 3 rank groups, 5 channel tiles
-    (8, 2, 64, 64, 128, 128, 128),      # r1 = 64: 16 rank groups, r3 = 64
+    (8, 2, 64, 64, 128, 128, 128),      # r1 = 64, E = 8: the expert form (E ranks)
+    (64, 2, 64, 64, 128, 128, 128),     # r1 = 64: 16 rank groups, r3 = 64
+    (4, 2, 6, 128, 192, 256, 256),      # E < r1: expert form on the persistent core (bf16)
+    (3, 2, 8, 128, 192, 256, 256),      # E = 3 < r1 = 8: bf16 keeps r1 (rank groups), fp32 E
 ]
 
 
