@@ -904,6 +904,42 @@ __device__ __forceinline__ float half_wave_sum(float v) {
   dpp_add_step<0x140>(v);   // row_mirror
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
 }
+// Over all 64 lanes (every lane active), the result in every lane: the 16-lane
+// DPP butterflies above, then the four rows' results (lanes 0, 16, 32, 48) read
+// into scalars and combined in row order. VALU and scalar reads only: no LDS
+// round trips, which a chain of __shfl_xor steps costs at each step.
+__device__ __forceinline__ float wave_sum(float v) {
+  dpp_add_step<0xb1>(v);    // quad_perm [1,0,3,2]
+  dpp_add_step<0x4e>(v);    // quad_perm [2,3,0,1]
+  dpp_add_step<0x141>(v);   // row_half_mirror
+  dpp_add_step<0x140>(v);   // row_mirror
+  const int b = __float_as_int(v);
+  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) +
+          __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) +
+          __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t key) {
+  dpp_max_step<0xb1>(key);
+  dpp_max_step<0x4e>(key);
+  dpp_max_step<0x141>(key);
+  dpp_max_step<0x140>(key);   // row_mirror: lane i with 15 - i
+  uint64_t best = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, 16 * r);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), 16 * r);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    best = o > best ? o : best;
+  }
+  return best;
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int lane_value(int v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
 template <int G>
 __device__ __forceinline__ void group_sum(float& v) {
   if constexpr (G >= 2) dpp_add_step<0xb1>(v);

@@ -216,7 +216,16 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
   // plane, all loads issued before any is used and before the U_expert staging
   // barrier; then added in plane order
   float zr[4] = {0.f, 0.f, 0.f, 0.f}, lr[4] = {0.f, 0.f, 0.f, 0.f};
+  float gv[4] = {0.f, 0.f, 0.f, 0.f}, zs[4] = {1.f, 1.f, 1.f, 1.f};
   if (live) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = lane + 64 * q;
+      if (j < R3) {
+        gv[q] = a.gain[j];
+        if (a.zscale) zs[q] = a.zscale[j];
+      }
+    }
     const float* row = raw + t * (R3 + E);
     float zp[kMaxFrontPlanes][4], lp[kMaxFrontPlanes][4];
 #pragma unroll
@@ -248,19 +257,18 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
     float v = 0.f;
     if (j < R3) {
       v = zr[q];
-      if (a.zscale) v *= a.zscale[j];
+      if (a.zscale) v *= zs[q];
     }
     zv[q] = v;
     ss += v * v;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  ss = wave_sum(ss);
   const float inv_rms = 1.f / sqrtf(ss / (float)R3 + a.eps);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int j = lane + 64 * q;
     if (j < R3)
-      store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, (zv[q] * inv_rms) * a.gain[j]);
+      store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, (zv[q] * inv_rms) * gv[q]);
   }
   uint64_t key[4];   // rank_key order; 0 past E and once taken
   float sv[4];       // the ranked scores (router_mode 1: capped ones)
@@ -281,13 +289,7 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
     uint64_t best = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) best = key[q] > best ? key[q] : best;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const uint32_t lo = __shfl_xor((uint32_t)best, off);
-      const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off);
-      const uint64_t o = ((uint64_t)hi << 32) | lo;
-      best = o > best ? o : best;
-    }
+    best = wave_max_key(best);
 #pragma unroll
     for (int q = 0; q < 4; ++q) key[q] = key[q] == best ? 0 : key[q];
     if (kk == lane) {   // k <= E: best names a candidate, index < E
@@ -295,21 +297,18 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
       si = key_index(best);
     }
   }
-  const float vmax = __shfl(selv, 0);
+  const float vmax = lane_value(selv, 0);
   const float ex = lane < K ? expf(selv - vmax) : 0.f;
-  float ssum = ex;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ssum += __shfl_xor(ssum, off);
+  const float ssum = wave_sum(ex);
   float wk;
   if (mode) {
     // softmax over all E, then the selected renormalised (+1e-6)
     float sa = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) sa += lane + 64 * q < E ? expf(sv[q] - vmax) : 0.f;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sa += __shfl_xor(sa, off);
+    sa = wave_sum(sa);
     float ps = 0.f;
-    for (int j = 0; j < K; ++j) ps += __shfl(ex, j) / sa;
+    for (int j = 0; j < K; ++j) ps += lane_value(ex, j) / sa;
     wk = (ex / sa) / (ps + 1e-6f);
   } else {
     wk = ex / ssum;
@@ -321,8 +320,8 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
   float cr = 0.f;
 #pragma unroll 1
   for (int kk = 0; kk < K; ++kk) {
-    const float w = __shfl(wk, kk);
-    const int i = __shfl(si, kk);
+    const float w = lane_value(wk, kk);
+    const int i = lane_value(si, kk);
     if (lane < R1) cr += w * ue[i * R1 + lane];
   }
   if (lane < R1) a.c[t * R1 + lane] = cr;
