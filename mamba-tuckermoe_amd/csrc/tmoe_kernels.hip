@@ -58,9 +58,11 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
                          (const float*)a.raw, a.front_split, stride);
       return hipGetLastError();
     }
-    // fewer 64-token tiles than compute units: tiles of 32 tokens, twice the
-    // work-groups (each streams the weight rows once more from L2)
-    if ((int64_t)cdiv(a.T, BM) < cu_count()) {
+    // tiles of 32 tokens when they all fit in one round of the compute units: a
+    // 32-token work-group takes ~0.9 of a 64-token one's time (both stream every
+    // weight row from L2), so half-filled second rounds lose (T = 12288: 50 us
+    // against 33 us with 192 work-groups of 64 tokens)
+    if ((int64_t)cdiv(a.T, 32) <= cu_count()) {
       constexpr int kStage32 = (32 + R3 + 32 * NR) * 128;
       constexpr int NS32 = 3 * kStage32 <= 160 * 1024 ? 3 : 2;
       hipLaunchKernelGGL((dev::k_front<Elt, R3, NR, kFrontPFA, 32, NS32, 1>), dim3(cdiv(a.T, 32)),
@@ -80,7 +82,7 @@ hipError_t launch_front_pair_nr(const FwdArgs& a0, const FwdArgs& a1, hipStream_
   if constexpr (NR < 8 && std::is_same<Elt, EltBF16>::value) {
     if (a0.front_split == 1 && a1.front_split == 1 && a0.T == a1.T) {
       constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-      if ((int64_t)cdiv(a0.T, kFrontBM) < cu_count()) {
+      if (2 * (int64_t)cdiv(a0.T, 32) <= cu_count()) {   // one round, as in launch_front_nr
         constexpr int kStage32 = (32 + R3 + 32 * NR) * 128;
         constexpr int NS32 = 3 * kStage32 <= 160 * 1024 ? 3 : 2;
         const int nt = (int)cdiv(a0.T, 32);
