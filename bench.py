@@ -134,9 +134,8 @@ def bench_ffn(args) -> None:
     m0 = sets[0][0]
     executed = 0
     for n in ("ffn_gate", "ffn_up", "ffn_down"):
-        fl = f.layer(n).flops(T)
-        rk = getattr(m0, n).plan().core_rank()
-        executed += fl["total"] - fl["core"] + fl["core"] * rk // f.r1
+        pl = getattr(m0, n).plan()
+        executed += f.layer(n).flops_executed(T, pl.core_rank(), pl.folded() and T > 256)["total"]
     peak = PEAK_TFLOPS[dt_name]
     tflops = flops / (ms * 1e-3) / 1e12
     tflops_exec = executed / (ms * 1e-3) / 1e12
@@ -266,6 +265,8 @@ def main():
                          "copy kernel of known size, to scale profiler byte counters)")
     ap.add_argument("--ffn", default=None,
                     help="time the FFN sub-block of this FFN workload (F0, F1, F2) instead")
+    ap.add_argument("--no-fold", action="store_true",
+                    help="keep the core and the out-projection as two GEMMs (TMOE_FLAG_NO_FOLD)")
     ap.add_argument("--latent", action="store_true",
                     help="time FusedLatentMoE forward + backward (training path) instead")
     args = ap.parse_args()
@@ -314,11 +315,17 @@ def main():
     x0 = pkg.synth.make_x(w)
     m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
     m.load_state_dict({k: v.to(dev) for k, v in params.items()})
+    m.set_fold(not args.no_fold)
     if codes is not None:
         m.load_fp8(*[codes[k].to(dev) for k in ("U_in_q", "U_in_scale", "core_q", "core_scale",
                                                   "U_out_q", "U_out_scale")])
     plan = m.plan()
     packed0 = m.packed()
+    folded = plan.folded() and T > 256   # T <= 256 runs the small-T kernels, never folded
+    rk = plan.core_rank()
+    form = ("folded: c (x) z against W = core U_out, one GEMM of width %d" % (rk * w.r3)
+            if folded else "two GEMMs: core (rank %d) then U_out" % rk)
+    log(f"[bench] plan form: {form}")
     ws_bytes = plan.workspace_bytes(T)
     set_bytes = T * w.d_in * es + T * w.d_out * es + ws_bytes + packed0.numel()
     n_sets = max(3, math.ceil(args.rotate_mb * 1e6 / set_bytes))
@@ -372,9 +379,10 @@ def main():
     finally:
         pkg._lib.prof_enable(False)
     stage_avg_us = {n: stage_ms[j] / calls * 1e3 for j, n in enumerate(pkg._lib.STAGE_NAMES)}
-    fl = w.flops()
+    fl_algo = w.flops()
+    fl = w.flops_executed(T, rk, folded)        # the dominant kernel's own work
     fl["front"] = fl["router"] + fl["in_proj"]   # one kernel computes both
-    sb = w.stage_bytes()
+    sb = w.stage_bytes_folded(T, rk) if folded else w.stage_bytes()
     dom = max(stage_avg_us, key=stage_avg_us.get)
     dom_tflops = fl[dom] / (stage_avg_us[dom] * 1e-6) / 1e12
     dom_gbs = sb[dom] / (stage_avg_us[dom] * 1e-6) / 1e9
@@ -382,11 +390,13 @@ def main():
     # the bound of the dominant kernel: MFMA when its arithmetic intensity is above
     # the ridge (peak flop/s over HBM bytes/s), HBM otherwise
     mfma_bound = fl[dom] / sb[dom] >= peak * 1e12 / (HBM_PEAK_GBS * 1e9)
-    layer_tflops = fl["total"] / (ms_per_step * 1e-3) / 1e12
+    layer_tflops = fl_algo["total"] / (ms_per_step * 1e-3) / 1e12
+    layer_exec_tflops = fl["total"] / (ms_per_step * 1e-3) / 1e12
     log("[bench] per-stage avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in stage_avg_us.items()))
     log(f"[bench] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak, "
         f"{dom_gbs:.1f} GB/s = {dom_gbs / HBM_PEAK_GBS:.3f} of HBM; "
-        f"layer {layer_tflops:.1f} TFLOP/s = {layer_tflops / peak:.3f} of peak")
+        f"layer {layer_tflops:.1f} TFLOP/s = {layer_tflops / peak:.3f} of peak (algorithmic), "
+        f"{layer_exec_tflops:.1f} executed")
 
     if args.copy_calibration_mib:
         n = args.copy_calibration_mib << 20
@@ -397,7 +407,8 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: 3 x {args.copy_calibration_mib} MiB device copies")
 
-    traffic = traffic_per_launch(w.name, dom) if T == pkg.WORKLOADS[w.name].T else None
+    traffic = (traffic_per_launch(w.name, dom + ("_folded" if folded else ""))
+               if T == pkg.WORKLOADS[w.name].T else None)
 
     # -- parity on a slice (GPU result of set 0 vs the fp32 reference path) --------
     from oracle import tucker_moe_np as onp
@@ -461,7 +472,8 @@ def main():
                    "d_in": w.d_in, "d_out": w.d_out, "E": w.E, "top_k": w.k,
                    "r1": w.r1, "r3": w.r3, "r2": w.r2, "rotated_sets": n_sets,
                    "weights": ("U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales, "
-                               "unpacked exactly to bf16; bf16 MFMA" if w.fp8 else dt_name)},
+                               "unpacked exactly to bf16; bf16 MFMA" if w.fp8 else dt_name),
+                   "form": form},
         "roofline": ({"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,
                       "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
                       "avg_us": stage_avg_us[dom], "flops_per_launch": fl[dom]}
@@ -470,6 +482,8 @@ def main():
                       "unit": "GB/s", "frac": dom_gbs / HBM_PEAK_GBS, "traffic": traffic,
                       "avg_us": stage_avg_us[dom], "bytes_per_launch": sb[dom]}),
         "layer": {"tflops": layer_tflops, "mfma_frac": layer_tflops / peak,
+                  "flops_per_step": fl_algo["total"],
+                  "executed_tflops": layer_exec_tflops, "executed_flops_per_step": fl["total"],
                   "hbm_gbs_compulsory": w.hbm_bytes() / (ms_per_step * 1e-3) / 1e9,
                   "stage_avg_us": stage_avg_us},
         "parity": parity,

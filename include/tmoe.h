@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 7
+#define TMOE_ABI_VERSION 8
 
 /* error codes */
 #define TMOE_OK            0
@@ -66,6 +66,9 @@ extern "C" {
  * scores, taken at the selected experts and divided by (their sum + 1e-6). The
  * reference's inference values are router_scale = 10, router_temperature = 0.5; both
  * must be > 0 (unused in mode 0). */
+/* plan flags (tmoe_shape.flags) */
+#define TMOE_FLAG_NO_FOLD 1  /* keep the core and the out-projection as two GEMMs */
+
 typedef struct tmoe_shape {
   int64_t d_in, d_out;
   int64_t E, k;
@@ -75,6 +78,7 @@ typedef struct tmoe_shape {
   float   eps;
   int32_t router_mode;
   float   router_scale, router_temperature;
+  int32_t flags;   /* TMOE_FLAG_* (0: the library chooses) */
 } tmoe_shape;
 
 typedef struct tmoe_plan tmoe_plan;
@@ -105,6 +109,22 @@ size_t tmoe_packed_bytes(const tmoe_plan* plan);
  * of the core's multiply-adds. No counterpart in the reference (its module always
  * forms the per-token expert matrices). */
 int64_t tmoe_plan_core_rank(const tmoe_plan* plan);
+
+/* 1 if the plan's large-T forward (T > 256) runs the folded form, else 0 (also for a
+ * null plan). The layer is linear after the routing, so with c = sum_j w_j
+ * U_expert[e_j] (model.py:91-93) and z the normalised in-projection (:80-81),
+ *   out = sum_r c_r (z core_r) U_out + bias = (c (x) z) W + bias,
+ *   W = core viewed as (r1*r3, r2) times U_out: (r1*r3, d_out),
+ * with (c (x) z)[t, r*r3 + s] = c[t, r] z[t, s] (the Khatri-Rao row product).
+ * tmoe_pack_weights then also packs W (summed in fp32 over r2, rounded once to
+ * bf16; fp8 plans fold the dequantised core and U_out), and the forward writes
+ * c (x) z (T, r1*r3) in place of mid and runs one GEMM against W. Chosen for bf16
+ * and fp8-weight plans when it takes fewer multiply-adds per token,
+ * r1*r3*d_out < r1*r3*r2 + r2*d_out (the reference's ranks (4, 1024, 256):
+ * 2.36 M against 3.41 M), unless shape.flags has TMOE_FLAG_NO_FOLD. No counterpart
+ * in the reference, which contracts z with the per-token core (model.py:87-98)
+ * and then projects through U_out (:101). T <= 256 always runs the unfolded form. */
+int tmoe_plan_folded(const tmoe_plan* plan);
 
 /* Version of the packed-weight layout that tmoe_pack_weights / _fp8 write and
  * tmoe_forward reads. No counterpart in the reference (whose checkpoints hold the

@@ -19,11 +19,12 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
 TMOE_EPI_NONE, TMOE_EPI_GLU, TMOE_EPI_RESIDUAL_SCALE = 0, 1, 2
+TMOE_FLAG_NO_FOLD = 1
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
 
@@ -31,7 +32,7 @@ STAGE_NAMES = ("front", "core", "out_proj")
 EXPORTED = (
     "tmoe_abi_version", "tmoe_last_error", "tmoe_plan_create", "tmoe_plan_destroy",
     "tmoe_packed_bytes", "tmoe_packed_layout_version", "tmoe_workspace_bytes",
-    "tmoe_plan_core_rank",
+    "tmoe_plan_core_rank", "tmoe_plan_folded",
     "tmoe_pack_weights", "tmoe_pack_weights_fp8",
     "tmoe_forward", "tmoe_forward_epi", "tmoe_forward_glu", "tmoe_rmsnorm_rows",
     "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
@@ -47,7 +48,7 @@ class TmoeShape(ctypes.Structure):
         ("r1", ctypes.c_int64), ("r2", ctypes.c_int64), ("r3", ctypes.c_int64),
         ("dtype", ctypes.c_int32), ("eps", ctypes.c_float),
         ("router_mode", ctypes.c_int32), ("router_scale", ctypes.c_float),
-        ("router_temperature", ctypes.c_float),
+        ("router_temperature", ctypes.c_float), ("flags", ctypes.c_int32),
     ]
 
 
@@ -90,6 +91,8 @@ def lib() -> ctypes.CDLL:
         L.tmoe_packed_bytes.argtypes = [vp]
         L.tmoe_plan_core_rank.restype = ctypes.c_int64
         L.tmoe_plan_core_rank.argtypes = [vp]
+        L.tmoe_plan_folded.restype = ctypes.c_int
+        L.tmoe_plan_folded.argtypes = [vp]
         L.tmoe_packed_layout_version.restype = ctypes.c_int
         L.tmoe_packed_layout_version.argtypes = []
         L.tmoe_workspace_bytes.restype = sz
@@ -147,7 +150,8 @@ class Plan:
     """Owns a tmoe_plan*. Immutable; safe to share across streams."""
 
     def __init__(self, d_in, d_out, E, k, r1, r2, r3, dtype: torch.dtype, eps: float,
-                 fp8_weights: bool = False, router=(TMOE_ROUTER_SOFTMAX_TOPK, 10.0, 0.5)):
+                 fp8_weights: bool = False, router=(TMOE_ROUTER_SOFTMAX_TOPK, 10.0, 0.5),
+                 flags: int = 0):
         if fp8_weights:
             if dtype != torch.bfloat16:
                 raise TmoeError(TMOE_EUNSUPPORTED,
@@ -161,7 +165,8 @@ class Plan:
             raise TmoeError(TMOE_EUNSUPPORTED,
                             f"parameter dtype {dtype}: supported are bfloat16 and float32")
         self.shape = TmoeShape(d_in, d_out, E, k, r1, r2, r3, code, eps, int(router[0]),
-                               float(router[1]), float(router[2]))
+                               float(router[1]), float(router[2]), int(flags))
+        self.flags = int(flags)
         self.router = tuple(router)
         self.dtype = dtype
         self.fp8_weights = fp8_weights
@@ -183,6 +188,10 @@ class Plan:
     def core_rank(self) -> int:
         """Rank of the core contraction the kernels run (r1, or E in the expert form)."""
         return int(lib().tmoe_plan_core_rank(self._ptr))
+
+    def folded(self) -> bool:
+        """True if T > 256 runs one GEMM of c (x) z against W = core U_out."""
+        return bool(lib().tmoe_plan_folded(self._ptr))
 
     def __del__(self):
         ptr, self._ptr = getattr(self, "_ptr", None), None

@@ -63,6 +63,22 @@ class Workload:
         st["total"] = sum(st.values())
         return st
 
+    def flops_executed(self, T: Optional[int] = None, rk: Optional[int] = None,
+                       folded: bool = False) -> dict:
+        """MFMA work the kernels run per forward, per stage: with the plan's core rank
+        rk (r1, or E in the expert form); a folded plan's core stage only forms the
+        Khatri-Rao rows c (x) z (no MFMA) and its out-projection contracts rk*r3."""
+        T = self.T if T is None else T
+        rk = self.r1 if rk is None else rk
+        st = {
+            "router": 2 * T * self.E * self.d_in,
+            "in_proj": 2 * T * self.d_in * self.r3,
+            "core": 0 if folded else 2 * T * rk * self.r3 * self.r2,
+            "out_proj": 2 * T * (rk * self.r3 if folded else self.r2) * self.d_out,
+        }
+        st["total"] = sum(st.values())
+        return st
+
     def stage_bytes(self, T: Optional[int] = None) -> dict:
         """Compulsory bytes per kernel stage: its inputs read once, its outputs
         written once (weights in the packed form the kernels read: the compute
@@ -83,6 +99,17 @@ class Workload:
             st["front"] += 4 * self.r3
             st["core"] += 8 * self.r1 * self.r2
             st["out_proj"] += 4 * self.d_out
+        return st
+
+    def stage_bytes_folded(self, T: Optional[int] = None, rk: Optional[int] = None) -> dict:
+        """stage_bytes of a folded plan: the core stage reads z and c and writes
+        c (x) z (T, rk*r3); the out-projection reads it and W^T (d_out, rk*r3) bf16."""
+        T = self.T if T is None else T
+        rk = self.r1 if rk is None else rk
+        st = self.stage_bytes(T)
+        K = rk * self.r3
+        st["core"] = T * self.r3 * 2 + T * rk * 4 + T * K * 2
+        st["out_proj"] = T * K * 2 + self.d_out * K * 2 + 4 * self.d_out + T * self.d_out * 2
         return st
 
     def hbm_bytes(self, T: Optional[int] = None) -> int:

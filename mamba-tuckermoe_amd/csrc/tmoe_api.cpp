@@ -34,6 +34,9 @@ struct tmoe_plan {
   // expert form (fewer experts than ranks, weights not fp8): U_expert packed as
   // the identity (E x E) and core as G_e = sum_r U_expert[e, r] core_r
   int64_t rk;
+  // folded form (large T): W^T (d_out, rk*r3) at off_fold, one GEMM of c (x) z against W
+  bool fold;
+  size_t off_fold;
 };
 
 namespace {
@@ -93,7 +96,10 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   L.c = o;   o = align256(o + (size_t)tile_rows * p->rk * sizeof(float));
   L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
   L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
-  L.mid = o; o = align256(o + (size_t)tile_rows * p->s.r2 * p->es);
+  // mid: (T, r2), or c (x) z (T, rk*r3) in a folded plan's large-T forward
+  const int64_t mid_cols =
+      p->fold && T > tmoe::kSmallT && p->rk * p->s.r3 > p->s.r2 ? p->rk * p->s.r3 : p->s.r2;
+  L.mid = o; o = align256(o + (size_t)tile_rows * mid_cols * p->es);
   L.raw = o;
   L.fsplit = tmoe::front_split(T, p->s.d_in, p->E_pad, p->kdtype == TMOE_BF16);
   if (T <= tmoe::kSmallT || L.fsplit > 1)
@@ -152,6 +158,35 @@ tmoe::FwdArgs make_args(const tmoe_plan* p, const void* x, int64_t T, const void
   return a;
 }
 
+// W^T of a folded plan from the packed core^T and U_out^T (fp8 plans: with the raw
+// core channel scales and the U_out column scales).
+hipError_t pack_fold(const tmoe_plan* p, char* base, hipStream_t st) {
+  const tmoe_shape& s = p->s;
+  auto f32at = [&](size_t off) { return reinterpret_cast<const float*>(base + off); };
+  return tmoe::launch_fold_out_t(reinterpret_cast<const uint16_t*>(base + p->off_core),
+                                 reinterpret_cast<const uint16_t*>(base + p->off_uout),
+                                 p->fp8w ? f32at(p->off_craw) : nullptr,
+                                 p->fp8w ? f32at(p->off_sout) : nullptr,
+                                 reinterpret_cast<uint16_t*>(base + p->off_fold), p->rk * s.r3,
+                                 s.r3, s.r2, s.d_out, st);
+}
+
+// A folded plan's large-T stages 2 and 3: c (x) z into mid, then the out-projection
+// kernel as one GEMM of width rk*r3 against W.
+tmoe::FwdArgs folded_args(const tmoe_plan* p, const tmoe::FwdArgs& a, const void* packed) {
+  tmoe::FwdArgs f = a;
+  f.r2 = p->rk * p->s.r3;
+  f.uoutT = static_cast<const char*>(packed) + p->off_fold;
+  f.out_scale = nullptr;
+  f.cz = tmoe::front_fuses_cz(f) ? f.mid : nullptr;
+  return f;
+}
+
+// stage 2 of a folded plan: c (x) z, unless the front already wrote it
+hipError_t launch_cz(const tmoe::FwdArgs& f, hipStream_t st) {
+  return f.cz ? hipSuccess : tmoe::launch_expand_cz(f, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -199,6 +234,8 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     return fail(TMOE_EUNSUPPORTED, "top_k=%lld: at most %d", (long long)s.k, tmoe::kMaxTopK);
   if (s.r1 > 64)
     return fail(TMOE_EUNSUPPORTED, "r1=%lld: at most 64", (long long)s.r1);
+  if (s.flags & ~TMOE_FLAG_NO_FOLD)
+    return fail(TMOE_EINVAL, "flags 0x%x: unknown bits", (unsigned)s.flags);
   // a GEMM tile (at most 512 operand rows of at most 4 MB) spans < 4 GB: the
   // kernels address it with 32-bit offsets
   if (s.d_in > (1 << 20) || s.r2 > (1 << 20))
@@ -239,6 +276,11 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   p->core_p = tmoe::core_p_supported(p->rk, s.r2, bf, p->fp8w);
   p->off_core_p = 0;
   if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)p->rk * s.r2 * s.r3 * p->es); }
+  // folded form: bf16 kernels, fewer multiply-adds per token
+  const int64_t K = p->rk * s.r3;
+  p->fold = bf && !(s.flags & TMOE_FLAG_NO_FOLD) && K * s.d_out < K * s.r2 + s.r2 * s.d_out;
+  p->off_fold = 0;
+  if (p->fold) { p->off_fold = o; o = align256(o + (size_t)s.d_out * K * p->es); }
   p->packed_bytes = o;
   *plan_out = p;
   return TMOE_OK;
@@ -250,10 +292,13 @@ size_t tmoe_packed_bytes(const tmoe_plan* plan) { return plan ? plan->packed_byt
 
 int64_t tmoe_plan_core_rank(const tmoe_plan* plan) { return plan ? plan->rk : 0; }
 
+int tmoe_plan_folded(const tmoe_plan* plan) { return plan && plan->fold ? 1 : 0; }
+
 // 1: front operand, gain, U_expert, core^T, U_out^T, bias, fp8 tables; 2: + P^T for
 // r1 in {1, 2, 4}; 3: P^T also for r1 = 4G in rank-group order; 4: plans with fewer
-// experts than ranks packed in the expert form (identity U_expert, core G).
-int tmoe_packed_layout_version(void) { return 4; }
+// experts than ranks packed in the expert form (identity U_expert, core G); 5: folded
+// plans add W^T = (core U_out)^T.
+int tmoe_packed_layout_version(void) { return 5; }
 
 size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T) {
   if (!plan || T < 0) return 0;
@@ -321,6 +366,7 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
   if ((e = tmoe::launch_to_f32(bias, reinterpret_cast<float*>(base + p->off_bias), s.d_out,
                                s.dtype, st)) != hipSuccess)
     return hip_fail(e, "pack bias");
+  if (p->fold && (e = pack_fold(p, base, st)) != hipSuccess) return hip_fail(e, "pack W (fold)");
   return TMOE_OK;
 }
 
@@ -383,6 +429,7 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
   if ((e = tmoe::launch_to_f32(core_scale, f32at(p->off_craw), s.r1 * s.r2, TMOE_F32, st)) !=
       hipSuccess)
     return hip_fail(e, "pack core scales");
+  if (p->fold && (e = pack_fold(p, base, st)) != hipSuccess) return hip_fail(e, "pack W (fold)");
   return TMOE_OK;
 }
 
@@ -425,7 +472,11 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
   hipStream_t st = static_cast<hipStream_t>(stream);
   using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
   const bool small = T <= tmoe::kSmallT;
-  const Launch big_path[kStages] = {tmoe::launch_front, tmoe::launch_core, tmoe::launch_outproj};
+  const bool fold = p->fold && !small;
+  if (fold) a = folded_args(p, a, packed);
+  const Launch big_path[kStages] = {tmoe::launch_front,
+                                    fold ? launch_cz : tmoe::launch_core,
+                                    tmoe::launch_outproj};
   const Launch small_path[kStages] = {tmoe::launch_small_front, tmoe::launch_small_core,
                                       tmoe::launch_small_out};
   const Launch* stages = small ? small_path : big_path;
@@ -479,8 +530,8 @@ int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* p
   u.epi_a = out;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
+  using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
   if (T <= tmoe::kSmallT) {
-    using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
     const Launch small[kStages] = {tmoe::launch_small_front, tmoe::launch_small_core,
                                    tmoe::launch_small_out};
     for (const tmoe::FwdArgs* a : {&g, &u})
@@ -488,8 +539,13 @@ int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* p
         if ((e = small[i](*a, st)) != hipSuccess) return hip_fail(e, "tmoe_forward_glu");
     return TMOE_OK;
   }
+  if (p->fold) {
+    g = folded_args(p, g, packed_gate);
+    u = folded_args(p, u, packed_up);
+  }
+  const Launch mid = p->fold ? launch_cz : tmoe::launch_core;
   if ((e = tmoe::launch_front_pair(g, u, st)) != hipSuccess ||
-      (e = tmoe::launch_core(g, st)) != hipSuccess || (e = tmoe::launch_core(u, st)) != hipSuccess ||
+      (e = mid(g, st)) != hipSuccess || (e = mid(u, st)) != hipSuccess ||
       (e = tmoe::launch_outproj(g, st)) != hipSuccess ||
       (e = tmoe::launch_outproj(u, st)) != hipSuccess)
     return hip_fail(e, "tmoe_forward_glu");

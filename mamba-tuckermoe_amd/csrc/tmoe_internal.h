@@ -48,7 +48,9 @@ struct FwdArgs {
   float* logits;                // (T, E) or null
   float* c;                     // (T, r1)
   void* z;                      // (T, r3)
-  void* mid;                    // (T, r2)
+  void* mid;                    // (T, r2); folded plans: c (x) z (T, r1*r3)
+  void* cz;                     // folded plans whose front writes c (x) z itself (= mid;
+                                //                      then z is not stored), else null
   float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
   float* mpart;                 // (S, T_pad, r2) fp32  k_core_pp with r1 > 4: partial sums
                                 //                      over rank groups (null otherwise)
@@ -145,6 +147,14 @@ hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
+// folded plans (T > kSmallT): mid (T, r1*r3) = c (x) z, the Khatri-Rao row product
+// mid[t, r*r3 + s] = c[t, r] z[t, s] rounded to bf16; launch_outproj then runs with
+// r2 := r1 * r3 and uoutT := W^T
+hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t stream);
+// Whether the large-T front kernel that launch_front picks for `a` can write c (x) z
+// itself (a.cz): the single-kind front (not the K-sliced one nor the split one of
+// the widest routers) with at most 32 ranks. Then no launch_expand_cz is needed.
+bool front_fuses_cz(const FwdArgs& a);
 // small-T path: front = skinny GEMM + per-token epilogue; core; out-projection
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t stream);
@@ -165,6 +175,13 @@ hipError_t launch_pack_core_p(const void* core, bool e4m3, const float* sc, uint
 // U_expert (E, r1) and core (r1, r3, r2), element size es (2: bf16, 4: fp32).
 hipError_t launch_mix_core_t(const void* uexp, const void* core, void* dst, int64_t E, int64_t r1,
                              int64_t r3, int64_t r2, int es, hipStream_t stream);
+// W^T (d_out, K) bf16 of a folded plan, K = rk * r3: W = core (K, r2) U_out (r2, d_out)
+// from the packed core^T (r2, K) and U_out^T (d_out, r2) (bf16 bits); with fp8
+// weights each core entry takes its channel scale cs[(kk / r3) * r2 + q] and each
+// output column the U_out scale os[n] (both null otherwise). fp32 sums, one rounding.
+hipError_t launch_fold_out_t(const uint16_t* coreT, const uint16_t* uoutT, const float* cs,
+                             const float* os, uint16_t* dst, int64_t K, int64_t r3, int64_t r2,
+                             int64_t d_out, hipStream_t stream);
 // dst (n, n) fp32 = identity
 hipError_t launch_eye(float* dst, int64_t n, hipStream_t stream);
 // core scale table (r1, r2) from the per-channel scales sc (r1, r2)

@@ -311,6 +311,39 @@ hipError_t launch_mix_core_t(const void* uexp, const void* core, void* dst, int6
   return hipGetLastError();
 }
 
+hipError_t launch_fold_out_t(const uint16_t* coreT, const uint16_t* uoutT, const float* cs,
+                             const float* os, uint16_t* dst, int64_t K, int64_t r3, int64_t r2,
+                             int64_t d_out, hipStream_t st) {
+  if (K == 0 || d_out == 0) return hipSuccess;
+  if (K % 32 || r2 % 32 || r3 % 32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dev::k_fold_out_t, dim3(cdiv(K, 32), cdiv(d_out, 32)), dim3(256), 0, st,
+                     coreT, uoutT, cs, os, dst, K, r3, r2, d_out);
+  return hipGetLastError();
+}
+
+bool front_fuses_cz(const FwdArgs& a) {
+  // launch_front_nr: k_front_split for r3 = 256 with E_pad = 256, k_front_part when
+  // front_split > 1, k_front (front_tile) otherwise; c fits over the logits for
+  // r1 <= 32 (BM x (E_pad + 1) floats)
+  return a.dtype == kDtypeBF16 && a.T > kSmallT && a.front_split == 1 && a.r1 <= 32 &&
+         !(a.r3 == 256 && a.E_pad == 256);
+}
+
+hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t st) {
+  if (a.dtype != kDtypeBF16) return hipErrorInvalidValue;
+  const int64_t n = a.T * (a.r3 / 8);   // threads: one 16-byte chunk of z each
+  if (n == 0) return hipSuccess;
+  if (n > ((int64_t)1 << 32) - 256) return hipErrorInvalidValue;
+  const dim3 grid(cdiv(n, 256)), block(256);
+  switch (a.r3) {
+    case 64: hipLaunchKernelGGL(dev::k_expand_cz<64>, grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL(dev::k_expand_cz<128>, grid, block, 0, st, a); break;
+    case 256: hipLaunchKernelGGL(dev::k_expand_cz<256>, grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_eye(float* dst, int64_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
   const dim3 grid(cdiv(n * n, 256) < 1024 ? cdiv(n * n, 256) : 1024), block(256);

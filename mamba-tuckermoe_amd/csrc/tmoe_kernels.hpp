@@ -1086,7 +1086,32 @@ __device__ __forceinline__ void front_z_epilogue(f32x16 (&acc)[TL::FM][TL::FN], 
       }
   }
   __syncthreads();
-  flush_tile<TL, T>(zst, reinterpret_cast<T*>(a.z) + m0 * R3, R3, rows_valid, R3);
+  // a front that writes c (x) z keeps the staged tile for that and stores no z
+  if (!a.cz) flush_tile<TL, T>(zst, reinterpret_cast<T*>(a.z) + m0 * R3, R3, rows_valid, R3);
+}
+
+// Folded plans: the Khatri-Rao rows of a front tile, cz[t][r R3 + s] = R(c[t][r] z[t][s]),
+// from the staged bf16 z tile (TileStage layout) and c (rows x rk floats in LDS), in
+// 16-byte chunks that run contiguously through the tile's rows of cz. Regular
+// (cached) stores: the out-projection reads them next.
+template <class TL, int R3>
+__device__ __forceinline__ void flush_cz(const char* zst, const float* cl, const FwdArgs& a,
+                                         int64_t m0, int rows_valid) {
+  constexpr int RB = TileStage<TL, uint16_t>::kRowBytes;
+  constexpr int CPR = R3 * 2 / 16;   // z chunks per row
+  const int rk = (int)a.r1;
+  uint16_t* dst = static_cast<uint16_t*>(a.cz) + m0 * rk * R3;
+  const int n = rows_valid * rk * CPR;
+  for (int q = threadIdx.x; q < n; q += TL::kThreads) {
+    const int ch = q % CPR, rr = q / CPR, row = rr / rk;
+    const u32x4 zv = *reinterpret_cast<const u32x4*>(zst + row * RB + ch * 16);
+    const float cr = cl[rr];   // rr = row * rk + r
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16x2(bf16_bits_to_f32(zv[j] & 0xffffu) * cr, bf16_bits_to_f32(zv[j] >> 16) * cr);
+    *reinterpret_cast<u32x4*>(dst + (int64_t)rr * R3 + ch * 8) = o;
+  }
 }
 
 // LDS floats of front_topk's per-row record: exp weights, indices and final
@@ -1107,7 +1132,8 @@ constexpr int kTopkRecFloats = BM * (3 * kMaxTopK + 2);
 // LDS when it fits in ue_bytes.
 template <int EP, int BM, int NT, int NP>
 __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int rows_valid,
-                                           const float* lg, int LD, float* rec, int ue_bytes) {
+                                           const float* lg, int LD, float* rec, int ue_bytes,
+                                           float* c_lds = nullptr) {
   constexpr int NWT = NT / 64;
   constexpr int kFill = NT / BM;
   constexpr int G = cmin(8, cmax(EP / 32, kFill < 1 ? 1 : kFill));
@@ -1192,6 +1218,7 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
     for (int kk = 0; kk < K; ++kk)
       cr += rec_w[row * kMaxTopK + kk] * uex[rec_i[row * kMaxTopK + kk] * R1 + r];
     a.c[(m0 + row) * R1 + r] = cr;
+    if (c_lds) c_lds[q] = cr;   // q = row * R1 + r
   }
 }
 
@@ -1247,8 +1274,16 @@ __device__ __forceinline__ void front_tile(const FwdArgs& a, int tile) {
           lg[row * LD + (wn * RX::RT + j) * 32 + (lane & 31)] = rx.racc[i][j][e];
       }
   front_z_epilogue<TL, Elt, R3>(acc, a, m0, rows_valid, zst, red);
+  // c goes to LDS over the logits (read before the top-k record is complete) when
+  // the tile also writes c (x) z: BM x r1 <= BM x (EP + 1) floats
   front_topk<EP, BM, TL::kThreads, kPlanes>(a, m0, rows_valid, lg, LD, red + NW * BM + BM,
-                                            kSmemBytes - kEpiBytes);
+                                            kSmemBytes - kEpiBytes, a.cz ? lg : nullptr);
+  if constexpr (std::is_same<Elt, EltBF16>::value) {
+    if (a.cz) {
+      __syncthreads();
+      flush_cz<TL, R3>(zst, lg, a, m0, rows_valid);
+    }
+  }
 }
 
 template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
@@ -1912,6 +1947,73 @@ __global__ __launch_bounds__(64 * WM * WN) void k_outproj_pp(FwdArgs a) {
 }
 
 // ---- packing kernels -----------------------------------------------------
+// W^T of a folded plan: dst[n][kk] = os[n] * sum_q uoutT[n][q] * coreT[q][kk] * cs[kk / r3][q]
+// (bf16 bits in and out, fp32 sums in q order, one rounding), i.e. W = core (K x r2)
+// times U_out (r2 x d_out) stored transposed (d_out rows of K). 32 x 32 output tiles,
+// 256 threads each holding 4 rows n; K and r2 are multiples of 32, d_out of 16.
+__global__ void k_fold_out_t(const uint16_t* __restrict__ coreT, const uint16_t* __restrict__ uoutT,
+                             const float* __restrict__ cs, const float* __restrict__ os,
+                             uint16_t* __restrict__ dst, int64_t K, int64_t r3, int64_t r2,
+                             int64_t d_out) {
+  __shared__ float ct[32][33];   // [q][kk]
+  __shared__ float ut[32][33];   // [n][q]
+  const int64_t k0 = (int64_t)blockIdx.x * 32, n0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8 threads
+  const int64_t rank = (k0 + tx) / r3;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t q0 = 0; q0 < r2; q0 += 32) {
+    for (int y = ty; y < 32; y += 8) {
+      float v = bf16_bits_to_f32(coreT[(q0 + y) * K + k0 + tx]);
+      if (cs) v *= cs[rank * r2 + q0 + y];
+      ct[y][tx] = v;
+      ut[y][tx] = n0 + y < d_out ? bf16_bits_to_f32(uoutT[(n0 + y) * r2 + q0 + tx]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int qq = 0; qq < 32; ++qq) {
+      const float c = ct[qq][tx];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(ut[ty + 8 * i][qq], c, acc[i]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + ty + 8 * i;
+    if (n < d_out) dst[n * K + k0 + tx] = f32_to_bf16_bits(os ? acc[i] * os[n] : acc[i]);
+  }
+}
+
+// The A operand of a folded plan's single GEMM: mid[t][r R3 + s] = R(c[t][r] * z[t][s])
+// (z bf16 (T, R3), c fp32 (T, rk), mid bf16 (T, rk R3)). A thread reads one 16-byte
+// chunk of z (8 elements) and writes its rk scaled copies; the R3 / 8 threads of a
+// row are consecutive, so each copy is stored as whole row segments.
+template <int R3>
+__global__ void k_expand_cz(const FwdArgs a) {
+  constexpr int CPR = R3 / 8;   // chunks per z row
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t t = i / CPR, s8 = (i % CPR) * 8;
+  if (t >= (uint64_t)a.T) return;
+  const int rk = (int)a.r1;
+  const u32x4 zv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.z) +
+                                                   (size_t)t * R3 + s8);
+  float zf[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    zf[2 * j] = bf16_bits_to_f32(zv[j] & 0xffffu);
+    zf[2 * j + 1] = bf16_bits_to_f32(zv[j] >> 16);
+  }
+  const float* crow = a.c + (size_t)t * rk;
+  uint16_t* dst = static_cast<uint16_t*>(a.mid) + (size_t)t * rk * R3 + s8;
+  for (int r = 0; r < rk; ++r) {
+    const float cr = crow[r];
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(zf[2 * j] * cr, zf[2 * j + 1] * cr);
+    *reinterpret_cast<u32x4*>(dst + r * R3) = o;
+  }
+}
+
 template <class T>
 __global__ void k_transpose(const T* __restrict__ src, T* __restrict__ dst, int64_t rows,
                             int64_t cols) {

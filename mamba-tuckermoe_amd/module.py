@@ -93,6 +93,7 @@ class TuckerMoE(nn.Module):
         self._warned_grad = False
         self._fp8: Optional[dict] = None   # e4m3 codes (uint8) and fp32 scales
         self._router = (_lib.TMOE_ROUTER_SOFTMAX_TOPK, 10.0, 0.5)
+        self._plan_flags = 0   # _lib.TMOE_FLAG_*: 0 lets the library choose the form
 
     # -- packed-weight cache -------------------------------------------------
     def _params(self):
@@ -112,14 +113,30 @@ class TuckerMoE(nn.Module):
         dtype = self.U_in.dtype
         fp8 = self._fp8 is not None
         if (self._plan is None or self._plan.dtype != dtype or self._plan.fp8_weights != fp8
-                or self._plan.router != self._router):
+                or self._plan.router != self._router or self._plan.flags != self._plan_flags):
             d_in, r3 = self.U_in.shape
             r2, d_out = self.U_out.shape
             E, r1 = self.U_expert.shape
             self._plan = _lib.Plan(d_in, d_out, E, self.top_k, r1, r2, r3, dtype,
                                    float(self.inner_norm.eps), fp8_weights=fp8,
-                                   router=self._router)
+                                   router=self._router, flags=self._plan_flags)
         return self._plan
+
+    def set_fold(self, enabled: bool = True) -> "TuckerMoE":
+        """Whether the library may fold the core into the out-projection (default).
+
+        The folded form computes the same layer as one GEMM of the Khatri-Rao rows
+        c (x) z against W = core U_out (packed once), chosen by the library when it
+        takes fewer multiply-adds per token; ``set_fold(False)`` keeps the core
+        contraction (model.py:87-98) and the out-projection (model.py:101) as two
+        GEMMs. Takes effect at the next forward (the weights are re-packed)."""
+        flags = 0 if enabled else _lib.TMOE_FLAG_NO_FOLD
+        if flags != self._plan_flags:
+            self._plan_flags = flags
+            self._plan = None
+            self._packed = None
+            self._packed_key = None
+        return self
 
     # -- router mode -------------------------------------------------------------
     def set_router_mode(self, mode: str = "softmax_topk", scale: float = 10.0,

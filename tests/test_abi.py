@@ -56,6 +56,7 @@ def _create(pkg, **kw):
     (dict(E=32, k=17), -2, "top_k=17"),
     (dict(r1=65), -2, "r1"),
     (dict(router_mode=2), -1, "router_mode"),
+    (dict(flags=2), -1, "flags"),
     (dict(router_mode=1, router_scale=0.0, router_temperature=0.5), -1, "router_scale"),
     (dict(router_mode=1, router_scale=10.0, router_temperature=-1.0), -1, "router_temperature"),
 ])
@@ -235,3 +236,40 @@ def test_plan_core_rank(pkg, kw, rank):
     finally:
         L.tmoe_plan_destroy(p)
     assert L.tmoe_plan_core_rank(None) == 0
+
+
+BF16 = 1
+FP8W = 2
+
+
+@pytest.mark.parametrize("kw,folded", [
+    # the BASELINE ranks (4, 1024, 256): 1024 * 2304 < 4 * 256 * 1024 + 1024 * 2304
+    (dict(d_in=1536, d_out=2304, E=16, k=2, r1=4, r2=1024, r3=256, dtype=BF16), 1),
+    (dict(d_in=1536, d_out=2304, E=256, k=8, r1=4, r2=1024, r3=256, dtype=BF16), 1),
+    (dict(d_in=1536, d_out=2304, E=16, k=2, r1=4, r2=1024, r3=256, dtype=FP8W), 1),
+    (dict(d_in=1536, d_out=2304, E=16, k=2, r1=4, r2=1024, r3=256, dtype=BF16, flags=1), 0),
+    # fp32 plans keep two GEMMs
+    (dict(d_in=512, d_out=1024, E=8, k=2, r1=4, r2=256, r3=128), 0),
+    # the deployed checkpoint ranks (32, 512, 256): 8192 * 4608 > 32 * 256 * 512 + 512 * 4608
+    (dict(d_in=768, d_out=4608, E=8, k=2, r1=32, r2=512, r3=256, dtype=BF16), 0),
+    # expert form (rank E = 8 < r1 = 64): folds over the E ranks, 8 * 64 * 128 < ...
+    (dict(d_in=128, d_out=128, E=8, k=2, r1=64, r2=128, r3=64, dtype=BF16), 1),
+])
+def test_plan_folded(pkg, kw, folded):
+    rc, p, msg = _create(pkg, **kw)
+    assert rc == 0, msg
+    L = pkg._lib.lib()
+    try:
+        assert L.tmoe_plan_folded(p) == folded
+        if folded:
+            # W^T (d_out, rk * r3) bf16 on top of the two-GEMM form's buffers
+            un = dict(kw, flags=1)
+            rc2, p2, msg2 = _create(pkg, **un)
+            assert rc2 == 0, msg2
+            rk = L.tmoe_plan_core_rank(p)
+            extra = L.tmoe_packed_bytes(p) - L.tmoe_packed_bytes(p2)
+            assert kw["d_out"] * rk * kw["r3"] * 2 <= extra < kw["d_out"] * rk * kw["r3"] * 2 + 256
+            L.tmoe_plan_destroy(p2)
+    finally:
+        L.tmoe_plan_destroy(p)
+    assert L.tmoe_plan_folded(None) == 0

@@ -18,10 +18,10 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
 
 
-def _module(pkg, dev, w, params):
+def _module(pkg, dev, w, params, fold=True):
     m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
     m.load_state_dict({k: v.to(dev) for k, v in params.items()})
-    return m
+    return m.set_fold(fold)
 
 
 def _run(m, x, dev):
@@ -54,29 +54,35 @@ def _check(w, got, ref64, label, torch_ref=None):
         assert same_t and err_t <= TOL[w.dtype], msg
 
 
+# fold=False keeps the core and the out-projection as two GEMMs (TMOE_FLAG_NO_FOLD);
+# the default lets the library fold them (bf16 plans of these shapes at T > 256)
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
 @pytest.mark.parametrize("name,T", [("C1", 64), ("C2", 32), ("C3", 1024), ("C4", 512)])
 @pytest.mark.parametrize("affine", ["unit", "random"])
-def test_workload_parity(pkg, dev, name, T, affine):
+def test_workload_parity(pkg, dev, name, T, affine, fold):
     w = pkg.WORKLOADS[name]
     params = pkg.synth.make_params(w, affine=affine)
     x = pkg.synth.make_x(w, T)
-    got = _run(_module(pkg, dev, w, params), x, dev)
+    got = _run(_module(pkg, dev, w, params, fold), x, dev)
     ref64 = onp.forward_f64(x, params, w.k)
     tref = ot.forward(x, params, w.k, compute_dtype=torch.float32, intermediates=True)
-    _check(w, got, ref64, f"{name}/{affine}", tref)
+    _check(w, got, ref64, f"{name}/{affine}/fold={fold}", tref)
 
 
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
 @pytest.mark.parametrize("name", ["C3", "C4"])
-def test_full_size(pkg, dev, name):
+def test_full_size(pkg, dev, name, fold):
     """BASELINE's full T, against the float64 oracle on every token and the
     torch fp32 restatement on the first 512."""
     w = pkg.WORKLOADS[name]
     params = pkg.synth.make_params(w)
     x = pkg.synth.make_x(w)
-    got = _run(_module(pkg, dev, w, params), x, dev)
+    m = _module(pkg, dev, w, params, fold)
+    got = _run(m, x, dev)
+    assert m.plan().folded() == fold
     ref64 = onp.forward_f64(x, params, w.k)
     tref = ot.forward(x[:512], params, w.k, compute_dtype=torch.float32, intermediates=True)
-    _check(w, got, ref64, f"{name}/full", tref)
+    _check(w, got, ref64, f"{name}/full/fold={fold}", tref)
 
 
 @pytest.mark.parametrize("T", [1, 3, 63, 65, 255, 257, 1000])
@@ -118,6 +124,22 @@ def test_shapes(pkg, dev, shape, dtype, T):
     x = pkg.synth.make_x(w)
     got = _run(_module(pkg, dev, w, params), x, dev)
     _check(w, got, onp.forward_f64(x, params, w.k), f"shape {shape} {dtype}")
+
+
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "E%d_k%d_r%d-%d-%d_%dx%d" % s)
+def test_shapes_fold_choice(pkg, dev, shape, fold):
+    """Large-T bf16 with the fold allowed or forbidden: the folded form where the
+    library picks it (fewer multiply-adds), the two-GEMM form otherwise."""
+    E, k, r1, r3, r2, d_in, d_out = shape
+    w = pkg.Workload("custom", 600, d_in, d_out, E, k, r1, r3, r2, torch.bfloat16, 78)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    m = _module(pkg, dev, w, params, fold)
+    got = _run(m, x, dev)
+    rk = m.plan().core_rank()
+    assert m.plan().folded() == (fold and rk * r3 * d_out < rk * r3 * r2 + r2 * d_out)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"shape {shape} fold={m.plan().folded()}")
 
 
 def test_deterministic_and_batch_dims(pkg, dev):
@@ -179,22 +201,24 @@ def _fp8_reference(params, codes):
     return ref
 
 
-def _fp8_module(pkg, dev, w, params, codes):
-    m = _module(pkg, dev, w, params)
+def _fp8_module(pkg, dev, w, params, codes, fold=True):
+    m = _module(pkg, dev, w, params, fold)
     m.load_fp8(*[codes[k].to(dev) for k in ("U_in_q", "U_in_scale", "core_q", "core_scale",
                                               "U_out_q", "U_out_scale")])
     return m
 
 
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
 @pytest.mark.parametrize("affine", ["unit", "random"])
-def test_fp8_weights_parity(pkg, dev, affine):
+def test_fp8_weights_parity(pkg, dev, affine, fold):
     """C5: e4m3 U_in / core / U_out with per-output-channel scales, against the
-    oracle run on the dequantised weights (bf16 bar)."""
+    oracle run on the dequantised weights (bf16 bar); folded, W is formed from the
+    dequantised core and U_out."""
     w = pkg.WORKLOADS["C5"]
     params, codes, _ = pkg.synth.make_fp8_params(w, affine=affine)
     ref = _fp8_reference(params, codes)
     x = pkg.synth.make_x(w, 1024)
-    got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
+    got = _run(_fp8_module(pkg, dev, w, params, codes, fold), x, dev)
     ref64 = onp.forward_f64(x, ref, w.k)
     ref32 = {k: v.float() for k, v in ref.items()}
     tref = ot.forward(x, ref32, w.k, compute_dtype=torch.float32, intermediates=True)
@@ -225,7 +249,8 @@ def test_fp8_full_size(pkg, dev):
 
 @pytest.mark.parametrize("r1,r2", [(3, 320), (4, 256)])
 @pytest.mark.parametrize("T", [40, 300])
-def test_fp8_every_code_and_zero_scales(pkg, dev, T, r1, r2):
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+def test_fp8_every_code_and_zero_scales(pkg, dev, T, r1, r2, fold):
     """Every finite e4m3 code appears in each weight, with some channels' scales
     zero (and, for core, a zero scale between non-zero ones of the same column).
     r1 = 3 with r2 = 320 runs the rank-rescaling core on a partial last tile,
@@ -255,7 +280,7 @@ def test_fp8_every_code_and_zero_scales(pkg, dev, T, r1, r2):
     params = {k: v.to(torch.bfloat16) for k, v in p32.items()}
     ref = _fp8_reference(params, codes)
     x = pkg.synth.make_x(w)
-    got = _run(_fp8_module(pkg, dev, w, params, codes), x, dev)
+    got = _run(_fp8_module(pkg, dev, w, params, codes, fold), x, dev)
     _check(w, got, onp.forward_f64(x, ref, w.k), "fp8 codes/zero scales")
 
 
