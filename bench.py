@@ -135,7 +135,7 @@ def bench_ffn(args) -> None:
     executed = 0
     for n in ("ffn_gate", "ffn_up", "ffn_down"):
         pl = getattr(m0, n).plan()
-        executed += f.layer(n).flops_executed(T, pl.core_rank(), pl.folded() and T > 256)["total"]
+        executed += f.layer(n).flops_executed(T, pl.core_rank(), pl.folded())["total"]
     peak = PEAK_TFLOPS[dt_name]
     tflops = flops / (ms * 1e-3) / 1e12
     tflops_exec = executed / (ms * 1e-3) / 1e12
@@ -321,7 +321,7 @@ def main():
                                                   "U_out_q", "U_out_scale")])
     plan = m.plan()
     packed0 = m.packed()
-    folded = plan.folded() and T > 256   # T <= 256 runs the small-T kernels, never folded
+    folded = plan.folded()
     rk = plan.core_rank()
     form = ("folded: c (x) z against W = core U_out, one GEMM of width %d" % (rk * w.r3)
             if folded else "two GEMMs: core (rank %d) then U_out" % rk)

@@ -110,20 +110,20 @@ size_t tmoe_packed_bytes(const tmoe_plan* plan);
  * forms the per-token expert matrices). */
 int64_t tmoe_plan_core_rank(const tmoe_plan* plan);
 
-/* 1 if the plan's large-T forward (T > 256) runs the folded form, else 0 (also for a
- * null plan). The layer is linear after the routing, so with c = sum_j w_j
+/* 1 if the plan's forward runs the folded form, else 0 (also for a null plan). The layer is linear after the routing, so with c = sum_j w_j
  * U_expert[e_j] (model.py:91-93) and z the normalised in-projection (:80-81),
  *   out = sum_r c_r (z core_r) U_out + bias = (c (x) z) W + bias,
  *   W = core viewed as (r1*r3, r2) times U_out: (r1*r3, d_out),
  * with (c (x) z)[t, r*r3 + s] = c[t, r] z[t, s] (the Khatri-Rao row product).
  * tmoe_pack_weights then also packs W (summed in fp32 over r2, rounded once to
- * bf16; fp8 plans fold the dequantised core and U_out), and the forward writes
- * c (x) z (T, r1*r3) in place of mid and runs one GEMM against W. Chosen for bf16
+ * bf16; fp8 plans fold the dequantised core and U_out), and the forward runs one
+ * GEMM of c (x) z (T, r1*r3) against W: for T > 256 the rows are written in place of
+ * mid, for T <= 256 the out-projection forms them from z and c. Chosen for bf16
  * and fp8-weight plans when it takes fewer multiply-adds per token,
  * r1*r3*d_out < r1*r3*r2 + r2*d_out (the reference's ranks (4, 1024, 256):
  * 2.36 M against 3.41 M), unless shape.flags has TMOE_FLAG_NO_FOLD. No counterpart
  * in the reference, which contracts z with the per-token core (model.py:87-98)
- * and then projects through U_out (:101). T <= 256 always runs the unfolded form. */
+ * and then projects through U_out (:101). */
 int tmoe_plan_folded(const tmoe_plan* plan);
 
 /* Version of the packed-weight layout that tmoe_pack_weights / _fp8 write and

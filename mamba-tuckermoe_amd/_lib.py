@@ -190,7 +190,7 @@ class Plan:
         return int(lib().tmoe_plan_core_rank(self._ptr))
 
     def folded(self) -> bool:
-        """True if T > 256 runs one GEMM of c (x) z against W = core U_out."""
+        """True if the forward runs one GEMM of c (x) z against W = core U_out."""
         return bool(lib().tmoe_plan_folded(self._ptr))
 
     def __del__(self):

@@ -182,6 +182,8 @@ tmoe::FwdArgs folded_args(const tmoe_plan* p, const tmoe::FwdArgs& a, const void
   return f;
 }
 
+hipError_t launch_nothing(const tmoe::FwdArgs&, hipStream_t) { return hipSuccess; }
+
 // stage 2 of a folded plan: c (x) z, unless the front already wrote it
 hipError_t launch_cz(const tmoe::FwdArgs& f, hipStream_t st) {
   return f.cz ? hipSuccess : tmoe::launch_expand_cz(f, st);
@@ -472,13 +474,15 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
   hipStream_t st = static_cast<hipStream_t>(stream);
   using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
   const bool small = T <= tmoe::kSmallT;
-  const bool fold = p->fold && !small;
+  const bool fold = p->fold;
   if (fold) a = folded_args(p, a, packed);
   const Launch big_path[kStages] = {tmoe::launch_front,
                                     fold ? launch_cz : tmoe::launch_core,
                                     tmoe::launch_outproj};
-  const Launch small_path[kStages] = {tmoe::launch_small_front, tmoe::launch_small_core,
-                                      tmoe::launch_small_out};
+  // folded: the out-projection builds c (x) z from z and c itself (no core stage)
+  const Launch small_path[kStages] = {tmoe::launch_small_front,
+                                      fold ? launch_nothing : tmoe::launch_small_core,
+                                      fold ? tmoe::launch_small_out_kr : tmoe::launch_small_out};
   const Launch* stages = small ? small_path : big_path;
   const char* stage_names[kStages] = {"front (router + in-projection)", "core",
                                       "out-projection"};
@@ -531,17 +535,18 @@ int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* p
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
+  if (p->fold) {
+    g = folded_args(p, g, packed_gate);
+    u = folded_args(p, u, packed_up);
+  }
   if (T <= tmoe::kSmallT) {
-    const Launch small[kStages] = {tmoe::launch_small_front, tmoe::launch_small_core,
-                                   tmoe::launch_small_out};
+    const Launch small[kStages] = {
+        tmoe::launch_small_front, p->fold ? launch_nothing : tmoe::launch_small_core,
+        p->fold ? tmoe::launch_small_out_kr : tmoe::launch_small_out};
     for (const tmoe::FwdArgs* a : {&g, &u})
       for (int i = 0; i < kStages; ++i)
         if ((e = small[i](*a, st)) != hipSuccess) return hip_fail(e, "tmoe_forward_glu");
     return TMOE_OK;
-  }
-  if (p->fold) {
-    g = folded_args(p, g, packed_gate);
-    u = folded_args(p, u, packed_up);
   }
   const Launch mid = p->fold ? launch_cz : tmoe::launch_core;
   if ((e = tmoe::launch_front_pair(g, u, st)) != hipSuccess ||

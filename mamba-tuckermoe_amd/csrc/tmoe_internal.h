@@ -159,6 +159,9 @@ bool front_fuses_cz(const FwdArgs& a);
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_out(const FwdArgs& a, hipStream_t stream);
+// folded plans: out = (c (x) z) W + bias with c (x) z built from z and c in registers
+// (a.r2 = r1 * r3, a.uoutT = W^T); bf16 only
+hipError_t launch_small_out_kr(const FwdArgs& a, hipStream_t stream);
 
 // Weight packing helpers (stream-ordered).
 // dst(cols, rows) bf16 = e4m3 src(rows, cols)^T; with colscale, entries whose

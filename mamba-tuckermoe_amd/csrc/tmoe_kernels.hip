@@ -221,10 +221,10 @@ hipError_t launch_small_core_t(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int MF, class Elt>
+template <int MF, class Elt, bool KR = false>
 hipError_t launch_small_out_t(const FwdArgs& a, hipStream_t st) {
   const dim3 grid(cdiv(a.d_out, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
-  hipLaunchKernelGGL((dev::k_sk_out<Elt, MF, kSkW>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((dev::k_sk_out<Elt, MF, kSkW, KR>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
@@ -248,12 +248,20 @@ template <int MF, class Elt>
 struct SmallOut {
   static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_out_t<MF, Elt>(a, st); }
 };
+template <int MF, class Elt>
+struct SmallOutKR {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) {
+    if constexpr (std::is_same<Elt, EltBF16>::value) return launch_small_out_t<MF, Elt, true>(a, st);
+    return hipErrorInvalidValue;   // folded plans are bf16
+  }
+};
 
 }  // namespace
 
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t st) { return by_rows<SmallFront>(a, st); }
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t st) { return by_rows<SmallCore>(a, st); }
 hipError_t launch_small_out(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOut>(a, st); }
+hipError_t launch_small_out_kr(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOutKR>(a, st); }
 
 hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t st) {
   if (a0.dtype != kDtypeBF16 || a0.r3 != 256 || a0.E_pad != a1.E_pad || a0.r3 != a1.r3) {

@@ -350,8 +350,10 @@ __global__ __launch_bounds__(64 * W) void k_sk_core(FwdArgs a) {
   }
 }
 
-// out (T, d_out) = mid U_out (* U_out scales) + bias
-template <class Elt, int MF, int W>
+// out (T, d_out) = mid U_out (* U_out scales) + bias; with KR (folded plans) the A
+// operand is c (x) z built in registers from z and c (as k_sk_core's), a.r2 = r1 * r3
+// and a.uoutT = W^T
+template <class Elt, int MF, int W, bool KR = false>
 __global__ __launch_bounds__(64 * W) void k_sk_out(FwdArgs a) {
   typedef typename Elt::T T;
   __shared__ float red[SkLds<MF, W>::kFloats];
@@ -363,9 +365,16 @@ __global__ __launch_bounds__(64 * W) void k_sk_out(FwdArgs a) {
   const int c = threadIdx.x & 15;
   const float bias = c < cols_valid ? a.bias[n0 + c] : 0.f;
   const float sc = a.out_scale && c < cols_valid ? a.out_scale[n0 + c] : 1.f;
-  SkRows<Elt> as{reinterpret_cast<const char*>(a.mid) + m0 * rb, rb, rows_valid};
-  skinny_tile<Elt, MF, W, 1>(as, reinterpret_cast<const char*>(a.uoutT) + n0 * rb, rb,
-                             cols_valid, a.r2, red);
+  if constexpr (KR) {
+    SkKhatriRao<Elt> as{reinterpret_cast<const char*>(a.z) + m0 * a.r3 * (int64_t)sizeof(T),
+                        a.c + m0 * a.r1, (int)a.r1, (int)a.r3, rows_valid};
+    skinny_tile<Elt, MF, W, 1>(as, reinterpret_cast<const char*>(a.uoutT) + n0 * rb, rb,
+                               cols_valid, a.r2, red);
+  } else {
+    SkRows<Elt> as{reinterpret_cast<const char*>(a.mid) + m0 * rb, rb, rows_valid};
+    skinny_tile<Elt, MF, W, 1>(as, reinterpret_cast<const char*>(a.uoutT) + n0 * rb, rb,
+                               cols_valid, a.r2, red);
+  }
   for (int e = threadIdx.x; e < MF * 256; e += 64 * W) {
     const int row = e >> 4;
     if (row < rows_valid && c < cols_valid) {
