@@ -35,29 +35,34 @@ int cu_count();
 
 template <class Elt, int R3, int NR>
 hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
-  if constexpr (R3 == 256 && NR == 8 && std::is_same<Elt, EltBF16>::value) {
-    // z and router work-groups of 32 tokens (k_front_split), three LDS stages
-    const dim3 grid(2 * cdiv(a.T, 32)), block(256);
-    hipLaunchKernelGGL((dev::k_front_split<Elt, R3, NR, kFrontPFA, 3>), grid, block, 0, st, a);
-    return hipGetLastError();
-  }
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-  constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
-  constexpr int kStageBytes = (BM + R3 + 32 * NR) * 128;
-  constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
-  if constexpr (BM > 32 && std::is_same<Elt, EltBF16>::value) {
+  if constexpr (std::is_same<Elt, EltBF16>::value) {
     if (a.front_split > 1) {
-      // K slices (k_front_part), then the per-token epilogue over their planes
+      // K slices of 64-token tiles (k_front_part), then the per-token epilogue over
+      // their planes
+      constexpr int kStageBytes = (kFrontBM + R3 + 32 * NR) * 128;
+      constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
       const int64_t stride = a.T * (a.r3 + a.E);
-      hipLaunchKernelGGL((dev::k_front_part<Elt, R3, NR, kFrontPFA, BM, NS, WM>),
-                         dim3(cdiv(a.T, BM), a.front_split), dim3(64 * NW * WM), 0, st, a, a.raw,
-                         a.front_split);
+      hipLaunchKernelGGL((dev::k_front_part<Elt, R3, NR, kFrontPFA, kFrontBM, NS, kFrontWM>),
+                         dim3(cdiv(a.T, kFrontBM), a.front_split), dim3(64 * NW * kFrontWM), 0,
+                         st, a, a.raw, a.front_split);
       if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
       hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256),
                          (size_t)(a.E * a.r1) * sizeof(float), st, a,
                          (const float*)a.raw, a.front_split, stride);
       return hipGetLastError();
     }
+  }
+  if constexpr (R3 == 256 && NR == 8 && std::is_same<Elt, EltBF16>::value) {
+    // z and router work-groups of 32 tokens (k_front_split), three LDS stages
+    const dim3 grid(2 * cdiv(a.T, 32)), block(256);
+    hipLaunchKernelGGL((dev::k_front_split<Elt, R3, NR, kFrontPFA, 3>), grid, block, 0, st, a);
+    return hipGetLastError();
+  }
+  constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
+  constexpr int kStageBytes = (BM + R3 + 32 * NR) * 128;
+  constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
+  if constexpr (BM > 32 && std::is_same<Elt, EltBF16>::value) {
     // tiles of 32 tokens when they all fit in one round of the compute units: a
     // 32-token work-group takes ~0.9 of a 64-token one's time (both stream every
     // weight row from L2), so half-filled second rounds lose (T = 12288: 50 us
@@ -330,11 +335,13 @@ hipError_t launch_fold_out_t(const uint16_t* coreT, const uint16_t* uoutT, const
 }
 
 bool front_fuses_cz(const FwdArgs& a) {
-  // launch_front_nr: k_front_split for r3 = 256 with E_pad = 256, k_front_part when
-  // front_split > 1, k_front (front_tile) otherwise; c fits over the logits for
-  // r1 <= 32 (BM x (E_pad + 1) floats)
-  return a.dtype == kDtypeBF16 && a.T > kSmallT && a.front_split == 1 && a.r1 <= 32 &&
-         !(a.r3 == 256 && a.E_pad == 256);
+  // launch_front_nr: k_front_part + k_front_epi when front_split > 1 (the per-token
+  // epilogue writes c (x) z for any r1), else k_front_split for r3 = 256 with
+  // E_pad = 256 (z and router in separate work-groups: no), else k_front (front_tile:
+  // c fits over the logits for r1 <= 32, BM x (E_pad + 1) floats)
+  if (a.dtype != kDtypeBF16 || a.T <= kSmallT) return false;
+  if (a.front_split > 1) return true;
+  return a.r1 <= 32 && !(a.r3 == 256 && a.E_pad == 256);
 }
 
 hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t st) {

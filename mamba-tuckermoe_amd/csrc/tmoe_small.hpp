@@ -267,8 +267,8 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int j = lane + 64 * q;
-    if (j < R3)
-      store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, (zv[q] * inv_rms) * gv[q]);
+    zv[q] = round_as((zv[q] * inv_rms) * gv[q], Elt{});   // z as stored
+    if (j < R3 && !a.cz) store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, zv[q]);
   }
   uint64_t key[4];   // rank_key order; 0 past E and once taken
   float sv[4];       // the ranked scores (router_mode 1: capped ones)
@@ -325,6 +325,18 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
     if (lane < R1) cr += w * ue[i * R1 + lane];
   }
   if (lane < R1) a.c[t * R1 + lane] = cr;
+  if (a.cz) {   // folded plans: the Khatri-Rao row c (x) z in place of z
+    T* dst = static_cast<T*>(a.cz) + t * R1 * R3;
+#pragma unroll 1
+    for (int r = 0; r < R1; ++r) {
+      const float c_r = lane_value(cr, r);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = lane + 64 * q;
+        if (j < R3) store_from_f32(dst + r * R3 + j, c_r * zv[q]);
+      }
+    }
+  }
 }
 
 // mid (T, r2) = (c (x) z) core^T; fp8 weights: rank r's partial sums scaled by

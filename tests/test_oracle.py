@@ -372,3 +372,31 @@ def test_capped_router_planted_mistakes(mistake):
                    stages={"route": bad})
     f = onp.forward_f64(x, params, w.k, router=("capped", scale, temp))
     assert np.abs(t["w"].numpy() - f["w"]).max() > 1e-7
+
+
+@pytest.mark.parametrize("d", [dict(E=8, d_in=64, d_out=48, r1=4, r3=32, r2=40),
+                               dict(E=3, d_in=32, d_out=24, r1=8, r3=16, r2=20)])
+def test_folded_form_identity(d):
+    """The algebra the kernels' folded form (and the expert form) rely on, against
+    the reference op sequence: with c = sum_j w_j U_expert[e_j] and z the normalised
+    in-projection, out = (c (x) z) W + bias with W = core_(r1 r3, r2) U_out, and
+    = sum_j w_j z (G_{e_j} U_out) + bias with G_e = sum_r U_expert[e, r] core_r."""
+    p = _params(21, **d)
+    x = _x(21, 50, d["d_in"])
+    ref = ot.forward(x.double(), {k: v.double() for k, v in p.items()}, 2, intermediates=True)
+    f = onp.forward_f64(x, p, 2)
+    T, r1, r3, r2 = x.shape[0], d["r1"], d["r3"], d["r2"]
+    core = p["core"].double().numpy()
+    U_out, bias = p["U_out"].double().numpy(), p["bias"].double().numpy()
+    W = core.reshape(r1 * r3, r2) @ U_out
+    A = (f["c"][:, :, None] * f["z"][:, None, :]).reshape(T, r1 * r3)
+    folded = A @ W + bias
+    assert onp.rel_l2(folded, f["out"]) < 1e-12
+    assert onp.rel_l2(folded, ref["out"].numpy()) < 1e-12
+    G = np.einsum("er,rsq->esq", p["U_expert"].double().numpy(), core)
+    expert = bias + sum(f["w"][:, j, None] * np.einsum("ts,tsn->tn", f["z"], (G @ U_out)[f["idx"][:, j]])
+                        for j in range(2))
+    assert onp.rel_l2(expert, ref["out"].numpy()) < 1e-12
+    # a transposed core face breaks it
+    Wt = np.swapaxes(core, 1, 2).reshape(r1 * r3, r2) @ U_out if r3 == r2 else W[::-1]
+    assert onp.rel_l2(A @ Wt + bias, ref["out"].numpy()) > 1e-3
