@@ -81,9 +81,12 @@ constexpr int64_t kCorePScales = 4096;
 inline bool core_p_grouped(int64_t r1) { return r1 > 4; }
 // K slices of the large-T bf16 front (router widths E_pad <= 128): when its
 // 64-token tiles number at most a quarter of kCoreUnits and d_in spans at least 16
-// K tiles, enough slices (of at least 8 K tiles each, at most kMaxFrontPlanes) to
+// K tiles, enough slices (of at least kFrontSliceKTiles each, at most kMaxFrontPlanes) to
 // approach kCoreUnits work-groups.
 constexpr int64_t kFrontMinKTiles = 16;
+// K tiles per slice at least: 4 measured no faster at T = 512-4096 (d_in = 1536) and
+// puts T = 3072 into two rounds of work-groups (6 slices x 48 tiles)
+constexpr int64_t kFrontSliceKTiles = 8;
 constexpr int kMaxFrontPlanes = 8;
 inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
   // E_pad = 256 measured slower sliced (C4: front 44.6 us against 34.8 us for the
@@ -94,7 +97,7 @@ inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
   // the 32-token front is faster
   if (4 * tiles > 256 || nkt < kFrontMinKTiles) return 1;
   int64_t s = (256 + tiles - 1) / tiles;
-  if (s > nkt / 8) s = nkt / 8;
+  if (s > nkt / kFrontSliceKTiles) s = nkt / kFrontSliceKTiles;
   if (s > kMaxFrontPlanes) s = kMaxFrontPlanes;
   return s > 1 ? (int)s : 1;
 }

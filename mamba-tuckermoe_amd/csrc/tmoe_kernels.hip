@@ -346,10 +346,10 @@ bool front_fuses_cz(const FwdArgs& a) {
 
 hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t st) {
   if (a.dtype != kDtypeBF16) return hipErrorInvalidValue;
-  const int64_t n = a.T * (a.r3 / 8);   // threads: one 16-byte chunk of z each
+  const int64_t n = a.T * (a.r3 / 8);   // 16-byte chunks of z, one per thread and pass
   if (n == 0) return hipSuccess;
-  if (n > ((int64_t)1 << 32) - 256) return hipErrorInvalidValue;
-  const dim3 grid(cdiv(n, 256)), block(256);
+  const int64_t blocks = (n + 255) / 256;
+  const dim3 grid((unsigned)(blocks < (1 << 20) ? blocks : (1 << 20))), block(256);
   switch (a.r3) {
     case 64: hipLaunchKernelGGL(dev::k_expand_cz<64>, grid, block, 0, st, a); break;
     case 128: hipLaunchKernelGGL(dev::k_expand_cz<128>, grid, block, 0, st, a); break;

@@ -1987,30 +1987,34 @@ __global__ void k_fold_out_t(const uint16_t* __restrict__ coreT, const uint16_t*
 // The A operand of a folded plan's single GEMM: mid[t][r R3 + s] = R(c[t][r] * z[t][s])
 // (z bf16 (T, R3), c fp32 (T, rk), mid bf16 (T, rk R3)). A thread reads one 16-byte
 // chunk of z (8 elements) and writes its rk scaled copies; the R3 / 8 threads of a
-// row are consecutive, so each copy is stored as whole row segments.
+// row are consecutive, so each copy is stored as whole row segments. Grid-stride
+// over the T * R3 / 8 chunks.
 template <int R3>
 __global__ void k_expand_cz(const FwdArgs a) {
   constexpr int CPR = R3 / 8;   // chunks per z row
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t t = i / CPR, s8 = (i % CPR) * 8;
-  if (t >= (uint64_t)a.T) return;
   const int rk = (int)a.r1;
-  const u32x4 zv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.z) +
-                                                   (size_t)t * R3 + s8);
-  float zf[8];
+  const uint64_t n = (uint64_t)a.T * CPR;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t t = i / CPR;
+    const uint32_t s8 = (uint32_t)(i % CPR) * 8;
+    const u32x4 zv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.z) +
+                                                     t * R3 + s8);
+    float zf[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    zf[2 * j] = bf16_bits_to_f32(zv[j] & 0xffffu);
-    zf[2 * j + 1] = bf16_bits_to_f32(zv[j] >> 16);
-  }
-  const float* crow = a.c + (size_t)t * rk;
-  uint16_t* dst = static_cast<uint16_t*>(a.mid) + (size_t)t * rk * R3 + s8;
-  for (int r = 0; r < rk; ++r) {
-    const float cr = crow[r];
-    u32x4 o;
+    for (int j = 0; j < 4; ++j) {
+      zf[2 * j] = bf16_bits_to_f32(zv[j] & 0xffffu);
+      zf[2 * j + 1] = bf16_bits_to_f32(zv[j] >> 16);
+    }
+    const float* crow = a.c + t * rk;
+    uint16_t* dst = static_cast<uint16_t*>(a.mid) + t * rk * R3 + s8;
+    for (int r = 0; r < rk; ++r) {
+      const float cr = crow[r];
+      u32x4 o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(zf[2 * j] * cr, zf[2 * j + 1] * cr);
-    *reinterpret_cast<u32x4*>(dst + r * R3) = o;
+      for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(zf[2 * j] * cr, zf[2 * j + 1] * cr);
+      *reinterpret_cast<u32x4*>(dst + r * R3) = o;
+    }
   }
 }
 
