@@ -67,7 +67,9 @@ struct FwdArgs {
 // fused out-projection epilogues (TMOE_EPI_* of include/tmoe.h)
 constexpr int kEpiNone = 0, kEpiGlu = 1, kEpiResScale = 2;
 
-// Token counts up to kSmallT take the small-T path (tmoe_small.hpp).
+// Token counts up to kSmallT take the small-T path (tmoe_small.hpp). Measured at the
+// C3 shapes (folded): T = 256 takes 42.8 us there against 49.4 us on the large-tile
+// kernels (49 us for any T from 96 up), T = 512 59.0 us against 41-43 us.
 constexpr int64_t kSmallT = 256;
 
 // k_core_pp (the persistent core for bf16 plans): ranks r1 in {1, 2, 4}, r1 * r2 a
