@@ -471,7 +471,11 @@ def main():
         "config": {"workload": f"{w.name}: Tucker-MoE layer forward, one GPU", "T": T,
                    "d_in": w.d_in, "d_out": w.d_out, "E": w.E, "top_k": w.k,
                    "r1": w.r1, "r3": w.r3, "r2": w.r2, "rotated_sets": n_sets,
-                   "weights": ("U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales, "
+                   "weights": (("U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales; U_in "
+                                "unpacked exactly to bf16, W = core U_out formed from the "
+                                "dequantised weights and rounded once to bf16; bf16 MFMA")
+                               if w.fp8 and folded else
+                               "U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales, "
                                "unpacked exactly to bf16; bf16 MFMA" if w.fp8 else dt_name),
                    "form": form},
         "roofline": ({"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,

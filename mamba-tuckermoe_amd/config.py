@@ -103,7 +103,10 @@ class Workload:
 
     def stage_bytes_folded(self, T: Optional[int] = None, rk: Optional[int] = None) -> dict:
         """stage_bytes of a folded plan: the core stage reads z and c and writes
-        c (x) z (T, rk*r3); the out-projection reads it and W^T (d_out, rk*r3) bf16."""
+        c (x) z (T, rk*r3); the out-projection reads it and W^T (d_out, rk*r3) bf16.
+        Where the front writes c (x) z itself (no z, no core kernel) these bytes stay
+        attributed to the core stage; the front's and out-projection's figures are
+        those of the split kernels."""
         T = self.T if T is None else T
         rk = self.r1 if rk is None else rk
         st = self.stage_bytes(T)
