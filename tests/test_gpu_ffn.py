@@ -236,13 +236,16 @@ def test_outproj_subblock(pkg, dev, T):
 
 @pytest.mark.parametrize("T", [100, 2048, 4096])
 @pytest.mark.parametrize("same_plan", [True, False])
-def test_glu_pair_equals_two_calls(pkg, dev, T, same_plan):
+@pytest.mark.parametrize("d_ff", [None, 512], ids=["F2", "folded"])
+def test_glu_pair_equals_two_calls(pkg, dev, T, same_plan, d_ff):
     """tmoe_forward_glu (both fronts in one launch) gives, bit for bit, tmoe_forward of
     the gate then tmoe_forward_epi(GLU) of the up; layers whose plans differ (here r1)
-    take the two-call path inside glu_pair."""
+    take the two-call path inside glu_pair. d_ff = 512 makes the same-rank plans take
+    the folded form (W = core U_out: 1024 x 512 against 4 x 256 x 512 + 512 x 512)."""
     f = pkg.FFN_WORKLOADS["F2"]
-    wg = pkg.Workload("g", T, f.d, f.d_ff, f.E, f.k, f.r1, f.r3, f.r2, torch.bfloat16, 41)
-    wu = pkg.Workload("u", T, f.d, f.d_ff, f.E, f.k, f.r1 if same_plan else 2 * f.r1, f.r3,
+    dff = d_ff or f.d_ff
+    wg = pkg.Workload("g", T, f.d, dff, f.E, f.k, f.r1, f.r3, f.r2, torch.bfloat16, 41)
+    wu = pkg.Workload("u", T, f.d, dff, f.E, f.k, f.r1 if same_plan else 2 * f.r1, f.r3,
                       f.r2, torch.bfloat16, 42)
     mods = []
     for w in (wg, wu):
@@ -255,4 +258,5 @@ def test_glu_pair_equals_two_calls(pkg, dev, T, same_plan):
         g = mods[0](x)
         ref = mods[1].forward_raw(x, epi=pkg._lib.TMOE_EPI_GLU, epi_a=g)[0]
     torch.cuda.synchronize()
+    assert mods[0].plan().folded() == (d_ff is not None)
     assert torch.equal(h, ref)
