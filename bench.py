@@ -61,6 +61,55 @@ def traffic_per_launch(workload: str, kernel: str):
     return None
 
 
+def cpu_threads():
+    """Host threads for the CPU baseline: the process's CPU affinity
+    (os.sched_getaffinity), capped by OMP_NUM_THREADS when the host sets it (the
+    GPU box sets its CPU share there). Returns (threads, affinity count)."""
+    n_aff = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    n = min(n_aff, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else n_aff
+    return n, n_aff
+
+
+def cpu_baseline(fwd, x0, T, chunk, seconds, wl_name, dt_name, what, oracle_mode):
+    """Times fwd(x, chunk=...) on the host: one warm-up pass, then the median of 3
+    passes over a sample of whole chunks sized so the 4 passes take about
+    `seconds` (at most all T tokens). With oracle_mode, the same op sequence in
+    float32 on the bf16-valued inputs (the parity reference) is timed too."""
+    import torch
+    threads, n_aff = cpu_threads()
+    torch.set_num_threads(threads)
+    chunk = min(chunk, T)
+    t_a = time.perf_counter()
+    fwd(x0[:chunk], chunk=chunk)                       # sizes the sample
+    rate = chunk / (time.perf_counter() - t_a)
+    n_cpu = int(min(T, max(chunk, seconds * rate / 4)) // chunk * chunk)
+
+    def median3(**kw):
+        fwd(x0[:n_cpu], chunk=chunk, **kw)             # warm-up pass
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fwd(x0[:n_cpu], chunk=chunk, **kw)
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    cpu_s = median3()
+    out = {
+        "value": n_cpu / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": (f"first {n_cpu} of the {T} {wl_name} tokens, {dt_name} tensors, {what}, "
+                   f"chunks of {chunk}, 1 warm-up + median of 3 passes, torch "
+                   f"{torch.__version__} with {threads} threads (affinity {n_aff} CPUs) on "
+                   f"{cpu_model()}"),
+        "seconds": cpu_s, "tokens": n_cpu, "cpu_model": cpu_model(), "affinity_cpus": n_aff,
+    }
+    if oracle_mode:
+        s32 = median3(compute_dtype=torch.float32)
+        out["oracle_mode_f32"] = {"value": n_cpu / s32, "unit": "tokens/s", "seconds": s32,
+                                  "sample": "the same passes in float32 on the bf16-valued inputs"}
+    return out
+
+
 FFN_METRIC = "TransformerBlock FFN sub-block tokens/sec (norm, gate, up, silu*up, down, residual)"
 
 
@@ -166,20 +215,9 @@ def bench_ffn(args) -> None:
                            "rows routed alike in all three layers"}
     cpu = None
     if not args.no_cpu:
-        threads = torch.get_num_threads()
-        chunk = min(256, T)
-        t_a = time.perf_counter()
-        ft.ffn_forward(x0[:chunk], params, f.k, chunk=chunk)
-        rate = chunk / (time.perf_counter() - t_a)
-        n_cpu = int(min(T, max(chunk, args.cpu_seconds * rate)) // chunk * chunk)
-        t_a = time.perf_counter()
-        ft.ffn_forward(x0[:n_cpu], params, f.k, chunk=chunk)
-        cpu_s = time.perf_counter() - t_a
-        cpu = {"value": n_cpu / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": (f"first {n_cpu} of the {T} {f.name} tokens, {dt_name}, the reference "
-                          f"op sequence (oracle/tucker_ffn_torch), torch {torch.__version__} "
-                          f"with {threads} threads on {cpu_model()}"),
-               "seconds": cpu_s}
+        cpu = cpu_baseline(lambda xs, **kw: ft.ffn_forward(xs, params, f.k, **kw), x0, T, 256,
+                           args.cpu_seconds, f.name, dt_name,
+                           "reference op sequence (oracle/tucker_ffn_torch)", oracle_mode=False)
     print(json.dumps({
         "metric": FFN_METRIC, "value": tok_s, "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
@@ -434,26 +472,12 @@ def main():
     # -- host-CPU baseline (rank 0, N=1): the reference op sequence on the CPU --------
     cpu = None
     if not args.no_cpu:
-        threads = torch.get_num_threads()
-        chunk = min(512, T)   # tokens per CPU pass; the sample is whole chunks
-        xs = x0[:chunk]
-        t_a = time.perf_counter()
-        # fp8: the reference runs on the dequantised weights, held in bf16 as the
-        # module's parameters hold them
-        ot.forward(xs, params, w.k, chunk=chunk)            # warm-up, also sizes the sample
-        rate = chunk / (time.perf_counter() - t_a)
-        n_cpu = int(min(T, max(chunk, args.cpu_seconds * rate)) // chunk * chunk)
-        t_a = time.perf_counter()
-        ot.forward(x0[:n_cpu], params, w.k, chunk=chunk)
-        cpu_s = time.perf_counter() - t_a
-        cpu = {
-            "value": n_cpu / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"first {n_cpu} of the {T} {w.name} tokens, {dt_name} tensors, "
-                       f"reference op sequence (oracle/tucker_moe_torch), chunks of {chunk}, "
-                       f"torch {torch.__version__} with {threads} threads on {cpu_model()}"),
-            "seconds": cpu_s,
-        }
-        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s on {threads} threads ({n_cpu} tokens, {cpu_s:.1f} s)")
+        cpu = cpu_baseline(lambda xs, **kw: ot.forward(xs, params, w.k, **kw), x0, T, 512,
+                           args.cpu_seconds, f"{w.name}", dt_name,
+                           "reference op sequence (oracle/tucker_moe_torch)",
+                           oracle_mode=dt_name != "f32")
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads "
+            f"({cpu['tokens']} tokens, median of 3 passes {cpu['seconds']:.2f} s)")
 
     res = {
         "metric": METRIC,

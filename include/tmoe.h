@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 8
+#define TMOE_ABI_VERSION 9
 
 /* error codes */
 #define TMOE_OK            0
@@ -239,10 +239,13 @@ int tmoe_rmsnorm_rows(const void* x, int64_t T, int64_t d, const void* weight, f
  *   dx[b] = sum_j p[b,j] dout[b] G[idx[b,j]]^T,  dp[b,j] = dout[b] . (x[b] G[idx[b,j]]),
  *   dG[e] = sum_{b,j: idx[b,j] = e} p[b,j] x[b]^T dout[b].
  * dtype TMOE_BF16 or TMOE_F32 (products in fp32 accumulators, each output rounded
- * once); r3 in {64, 128, 256}, r2 a multiple of 64, 1 <= k <= min(E, 16), E <= 64.
+ * once), optionally OR'ed with TMOE_LATENT_P_F32: p and dp are then fp32 whatever
+ * dtype is (the reference's kernels read top_k_probs in their own dtype, and its
+ * dprobs has that dtype; model.py:160-174, :196-219, :250); r3 in {64, 128, 256}, r2 a multiple of 64, 1 <= k <= min(E, 16), E <= 64.
  * An index outside [0, E) selects nothing. All pointers device, 16-byte aligned;
  * workspace of at least tmoe_latent_workspace_bytes(...) bytes. B == 0 is a no-op.
  * Stream-ordered, no allocation, no host synchronisation. */
+#define TMOE_LATENT_P_F32 0x100
 size_t tmoe_latent_workspace_bytes(int64_t B, int64_t E, int64_t r3, int64_t r2, int dtype,
                                    int backward);
 int tmoe_latent_forward(const void* x, const void* G, const int64_t* idx, const void* p,

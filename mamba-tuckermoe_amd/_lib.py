@@ -19,12 +19,13 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
 TMOE_EPI_NONE, TMOE_EPI_GLU, TMOE_EPI_RESIDUAL_SCALE = 0, 1, 2
 TMOE_FLAG_NO_FOLD = 1
+TMOE_LATENT_P_F32 = 0x100   # or'ed into a latent call's dtype: p and dp are fp32
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
 

@@ -89,9 +89,11 @@ struct Layout {
 Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   Layout L{};
   size_t o = 0;
-  // k_core_pp reads c and stores mid in whole 256-token tiles
-  const int64_t tile_rows =
-      p->core_p ? (T + tmoe::kCorePRows - 1) / tmoe::kCorePRows * tmoe::kCorePRows : T;
+  // k_core_pp reads c and stores mid in whole 256-token tiles; a folded plan's
+  // out-projection reads its A operand (c (x) z in mid) in whole 256-row tiles
+  const int64_t tile_rows = p->core_p || p->fold
+                                ? (T + tmoe::kCorePRows - 1) / tmoe::kCorePRows * tmoe::kCorePRows
+                                : T;
   L.z = o;   o = align256(o + (size_t)T * p->s.r3 * p->es);
   L.c = o;   o = align256(o + (size_t)tile_rows * p->rk * sizeof(float));
   L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
@@ -275,12 +277,13 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     p->off_sout = o;   o = align256(o + (size_t)s.d_out * sizeof(float));
     p->off_craw = o;   o = align256(o + (size_t)s.r1 * s.r2 * sizeof(float));
   }
-  p->core_p = tmoe::core_p_supported(p->rk, s.r2, bf, p->fp8w);
-  p->off_core_p = 0;
-  if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)p->rk * s.r2 * s.r3 * p->es); }
   // folded form: bf16 kernels, fewer multiply-adds per token
   const int64_t K = p->rk * s.r3;
   p->fold = bf && !(s.flags & TMOE_FLAG_NO_FOLD) && K * s.d_out < K * s.r2 + s.r2 * s.d_out;
+  // P^T feeds only the unfolded core (k_core_pp); a folded forward never reads it
+  p->core_p = !p->fold && tmoe::core_p_supported(p->rk, s.r2, bf, p->fp8w);
+  p->off_core_p = 0;
+  if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)p->rk * s.r2 * s.r3 * p->es); }
   p->off_fold = 0;
   if (p->fold) { p->off_fold = o; o = align256(o + (size_t)s.d_out * K * p->es); }
   p->packed_bytes = o;
@@ -300,7 +303,7 @@ int tmoe_plan_folded(const tmoe_plan* plan) { return plan && plan->fold ? 1 : 0;
 // r1 in {1, 2, 4}; 3: P^T also for r1 = 4G in rank-group order; 4: plans with fewer
 // experts than ranks packed in the expert form (identity U_expert, core G); 5: folded
 // plans add W^T = (core U_out)^T.
-int tmoe_packed_layout_version(void) { return 5; }
+int tmoe_packed_layout_version(void) { return 6; }
 
 size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T) {
   if (!plan || T < 0) return 0;
@@ -395,8 +398,10 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
   auto f32at = [&](size_t off) { return reinterpret_cast<float*>(base + off); };
   auto bf16at = [&](size_t off) { return reinterpret_cast<uint16_t*>(base + off); };
   hipError_t e;
-  if ((e = tmoe::launch_transpose_e4m3(U_in_q, bf16at(p->off_front), s.d_in, s.r3, nullptr, 1,
-                                       st)) != hipSuccess)
+  // a zero scale packs its channel as zeros (whatever its codes, NaN included);
+  // U_in's and U_out's scales are per column: group = all rows
+  if ((e = tmoe::launch_transpose_e4m3(U_in_q, bf16at(p->off_front), s.d_in, s.r3, U_in_scale,
+                                       s.d_in, st)) != hipSuccess)
     return hip_fail(e, "pack U_in");
   if ((e = tmoe::launch_copy_pad(router_w, base + p->off_router, s.E * s.d_in,
                                  p->E_pad * s.d_in, 2, st)) != hipSuccess)
@@ -417,8 +422,8 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
       (e = tmoe::launch_pack_core_p(core_q, true, core_scale, bf16at(p->off_core_p), s.r1, s.r3,
                                     s.r2, st)) != hipSuccess)
     return hip_fail(e, "pack core (P layout)");
-  if ((e = tmoe::launch_transpose_e4m3(U_out_q, bf16at(p->off_uout), s.r2, s.d_out, nullptr, 1,
-                                       st)) != hipSuccess)
+  if ((e = tmoe::launch_transpose_e4m3(U_out_q, bf16at(p->off_uout), s.r2, s.d_out, U_out_scale,
+                                       s.r2, st)) != hipSuccess)
     return hip_fail(e, "pack U_out");
   if ((e = tmoe::launch_to_f32(bias, f32at(p->off_bias), s.d_out, TMOE_BF16, st)) != hipSuccess)
     return hip_fail(e, "pack bias");
@@ -491,18 +496,33 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
   std::unique_lock<std::mutex> lk(g_prof.mu);
   const bool prof = g_prof.on;
   if (!prof) lk.unlock();
+  // on an error the events taken so far go back to the pool (the lock is held)
+  auto release = [&](hipEvent_t extra) {
+    for (hipEvent_t e : ev) g_prof.free_ev.push_back(e);
+    if (extra) g_prof.free_ev.push_back(extra);
+    ev.clear();
+  };
   for (int i = 0; i < kStages; ++i) {
     if (prof) {
       hipEvent_t e = prof_event();
-      if (!e || hipEventRecord(e, st) != hipSuccess) return fail(TMOE_EHIP, "profiling event");
+      if (!e || hipEventRecord(e, st) != hipSuccess) {
+        release(e);
+        return fail(TMOE_EHIP, "profiling event");
+      }
       ev.push_back(e);
     }
     const hipError_t e = stages[i](a, st);
-    if (e != hipSuccess) return hip_fail(e, stage_names[i]);
+    if (e != hipSuccess) {
+      if (prof) release(nullptr);
+      return hip_fail(e, stage_names[i]);
+    }
   }
   if (prof) {
     hipEvent_t e = prof_event();
-    if (!e || hipEventRecord(e, st) != hipSuccess) return fail(TMOE_EHIP, "profiling event");
+    if (!e || hipEventRecord(e, st) != hipSuccess) {
+      release(e);
+      return fail(TMOE_EHIP, "profiling event");
+    }
     ev.push_back(e);
     g_prof.pending.push_back(std::move(ev));
   }
@@ -593,6 +613,7 @@ int latent_check(const char* who, int64_t B, int64_t E, int64_t k, int64_t r3, i
 
 size_t tmoe_latent_workspace_bytes(int64_t B, int64_t E, int64_t r3, int64_t r2, int dtype,
                                    int backward) {
+  dtype &= ~TMOE_LATENT_P_F32;
   if (B < 0 || E < 1 || r3 < 1 || r2 < 1 || (dtype != TMOE_BF16 && dtype != TMOE_F32)) return 0;
   return tmoe::latent_workspace_bytes(B, E, r3, r2, dtype == TMOE_BF16 ? 2 : 4, backward != 0);
 }
@@ -601,6 +622,8 @@ int tmoe_latent_forward(const void* x, const void* G, const int64_t* idx, const 
                         int64_t B, int64_t E, int64_t k, int64_t r3, int64_t r2, int dtype,
                         void* out, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
+  const bool p_f32 = (dtype & TMOE_LATENT_P_F32) != 0;
+  dtype &= ~TMOE_LATENT_P_F32;
   if (int rc = latent_check("tmoe_latent_forward", B, E, k, r3, r2, dtype)) return rc;
   if (B == 0) return TMOE_OK;
   if (!x || !G || !idx || !p || !out || !workspace)
@@ -612,7 +635,7 @@ int tmoe_latent_forward(const void* x, const void* G, const int64_t* idx, const 
     return fail(TMOE_EINVAL, "tmoe_latent_forward: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   tmoe::LatentArgs l{};
-  l.dtype = dtype; l.B = B; l.E = E; l.k = k; l.r3 = r3; l.r2 = r2;
+  l.dtype = dtype; l.p_f32 = p_f32; l.B = B; l.E = E; l.k = k; l.r3 = r3; l.r2 = r2;
   l.x = x; l.G = G; l.idx = idx; l.p = p; l.out = out; l.ws = workspace;
   const hipError_t e = tmoe::latent_forward(l, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_latent_forward");
@@ -623,6 +646,8 @@ int tmoe_latent_backward(const void* x, const void* G, const int64_t* idx, const
                          int64_t r2, int dtype, void* dx, void* dG, void* dp, void* workspace,
                          size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
+  const bool p_f32 = (dtype & TMOE_LATENT_P_F32) != 0;
+  dtype &= ~TMOE_LATENT_P_F32;
   if (int rc = latent_check("tmoe_latent_backward", B, E, k, r3, r2, dtype)) return rc;
   if (B == 0) return TMOE_OK;
   if (!x || !G || !idx || !p || !dout || !dx || !dG || !dp || !workspace)
@@ -636,7 +661,7 @@ int tmoe_latent_backward(const void* x, const void* G, const int64_t* idx, const
     return fail(TMOE_EINVAL, "tmoe_latent_backward: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   tmoe::LatentArgs l{};
-  l.dtype = dtype; l.B = B; l.E = E; l.k = k; l.r3 = r3; l.r2 = r2;
+  l.dtype = dtype; l.p_f32 = p_f32; l.B = B; l.E = E; l.k = k; l.r3 = r3; l.r2 = r2;
   l.x = x; l.G = G; l.idx = idx; l.p = p; l.dout = dout; l.dx = dx; l.dG = dG; l.dp = dp;
   l.ws = workspace;
   const hipError_t e = tmoe::latent_backward(l, static_cast<hipStream_t>(stream));

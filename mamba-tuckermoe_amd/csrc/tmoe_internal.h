@@ -129,6 +129,7 @@ inline bool core_p_supported(int64_t r1, int64_t r2, bool bf16, bool fp8w) {
 // dtype; outputs out (B, r2) or dx (B, r3), dG (E, r3, r2), dp (B, k).
 struct LatentArgs {
   int dtype;
+  bool p_f32;   // p and dp are fp32 (else dtype)
   int64_t B, E, k, r3, r2;
   const void* x;
   const void* G;

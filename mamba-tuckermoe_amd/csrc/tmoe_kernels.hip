@@ -526,7 +526,7 @@ hipError_t latent_forward(const LatentArgs& l, hipStream_t st) {
   const LatentLayout L = latent_layout(l.B, l.E, l.r3, l.r2, es, false);
   char* ws = static_cast<char*>(l.ws);
   float* w = reinterpret_cast<float*>(ws + L.w);
-  hipError_t e = bf ? latent_weights<uint16_t>(l, w, st) : latent_weights<float>(l, w, st);
+  hipError_t e = bf && !l.p_f32 ? latent_weights<uint16_t>(l, w, st) : latent_weights<float>(l, w, st);
   if (e != hipSuccess) return e;
   // G as (E r3, r2), transposed: the B^T operand (r2, E r3) of the Khatri-Rao GEMM
   if ((e = launch_transpose(l.G, ws + L.gt, l.E * l.r3, l.r2, es, st)) != hipSuccess) return e;
@@ -547,7 +547,7 @@ hipError_t latent_backward(const LatentArgs& l, hipStream_t st) {
   const int64_t M = l.E * l.r3;
   char* ws = static_cast<char*>(l.ws);
   float* w = reinterpret_cast<float*>(ws + L.w);
-  hipError_t e = bf ? latent_weights<uint16_t>(l, w, st) : latent_weights<float>(l, w, st);
+  hipError_t e = bf && !l.p_f32 ? latent_weights<uint16_t>(l, w, st) : latent_weights<float>(l, w, st);
   if (e != hipSuccess) return e;
   // H = dout G_flat^T (B, E r3): the out-projection GEMM with U_out^T := G as (E r3, r2)
   if ((e = launch_copy_pad(nullptr, ws + L.zero, 0, M, 4, st)) != hipSuccess) return e;
@@ -560,7 +560,12 @@ hipError_t latent_backward(const LatentArgs& l, hipStream_t st) {
   a.out = ws + L.h;
   if ((e = launch_outproj(a, st)) != hipSuccess) return e;
   // dx and dp from H
-  if (bf)
+  if (bf && l.p_f32)
+    hipLaunchKernelGGL((dev::k_latent_dx_dp<uint16_t, float>), dim3(cdiv(l.B, 4)), dim3(256), 0,
+                       st, reinterpret_cast<const uint16_t*>(ws + L.h), w,
+                       static_cast<const uint16_t*>(l.x), l.idx, l.B, (int)l.E, (int)l.k,
+                       (int)l.r3, static_cast<uint16_t*>(l.dx), static_cast<float*>(l.dp));
+  else if (bf)
     hipLaunchKernelGGL((dev::k_latent_dx_dp<uint16_t, uint16_t>), dim3(cdiv(l.B, 4)), dim3(256), 0,
                        st, reinterpret_cast<const uint16_t*>(ws + L.h), w,
                        static_cast<const uint16_t*>(l.x), l.idx, l.B, (int)l.E, (int)l.k,

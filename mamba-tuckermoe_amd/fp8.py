@@ -37,7 +37,9 @@ def quantize(w: torch.Tensor, name: str) -> Tuple[torch.Tensor, torch.Tensor]:
 
 
 def dequantize(q: torch.Tensor, scale: torch.Tensor, name: str) -> torch.Tensor:
-    """fp32 weight q * s of `name` (q as float8_e4m3fn or its uint8 bits)."""
+    """fp32 weight q * s of `name` (q as float8_e4m3fn or its uint8 bits); a
+    channel whose scale is zero is zero whatever its codes (NaN codes included),
+    as the packed weights hold it."""
     if q.dtype == torch.uint8:
         q = q.view(torch.float8_e4m3fn)
     s = scale.float()
@@ -47,7 +49,7 @@ def dequantize(q: torch.Tensor, scale: torch.Tensor, name: str) -> torch.Tensor:
         s = s.unsqueeze(0)          # (1, cols)
     else:
         raise ValueError(f"no fp8 layout for {name!r}")
-    return q.float() * s
+    return torch.where(s == 0, torch.zeros((), dtype=torch.float32, device=q.device), q.float() * s)
 
 
 def quantize_params(params: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:

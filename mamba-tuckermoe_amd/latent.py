@@ -50,11 +50,15 @@ class FusedLatentMoE(torch.autograd.Function):
         x = x_shared.contiguous()
         G = G_experts.contiguous()
         idx = top_k_indices.contiguous()
-        p = top_k_probs.to(x.dtype).contiguous()
+        # the reference's kernels read the probabilities in their own dtype
+        # (model.py:160-174, :196-219): fp32 ones reach the kernels unrounded, others
+        # in x's dtype
+        p_f32 = top_k_probs.dtype == torch.float32 and x.dtype != torch.float32
+        p = top_k_probs.to(torch.float32 if p_f32 else x.dtype).contiguous()
         B, r3 = x.shape
         E, _, r2 = G.shape
         k = idx.shape[1]
-        dt = _lib.dtype_code(x.dtype)
+        dt = _lib.dtype_code(x.dtype) | (_lib.TMOE_LATENT_P_F32 if p_f32 else 0)
         L = _lib.lib()
         out = torch.empty(B, r2, dtype=x.dtype, device=x.device)
         nws = L.tmoe_latent_workspace_bytes(B, E, r3, r2, dt, 0)
@@ -75,11 +79,12 @@ class FusedLatentMoE(torch.autograd.Function):
         E, _, r2 = G.shape
         k = idx.shape[1]
         d = dout.to(x.dtype).contiguous()
-        dt = _lib.dtype_code(x.dtype)
+        p_f32 = p.dtype == torch.float32 and x.dtype != torch.float32
+        dt = _lib.dtype_code(x.dtype) | (_lib.TMOE_LATENT_P_F32 if p_f32 else 0)
         L = _lib.lib()
         dx = torch.empty_like(x)
         dG = torch.empty_like(G)
-        dp = torch.empty(B, k, dtype=x.dtype, device=x.device)
+        dp = torch.empty(B, k, dtype=p.dtype, device=x.device)
         nws = L.tmoe_latent_workspace_bytes(B, E, r3, r2, dt, 1)
         ws = _ws(nws, x.device)
         with torch.cuda.device(x.device):

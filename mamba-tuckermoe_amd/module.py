@@ -14,9 +14,11 @@ library or an unsupported shape raises. The module is inference-only: its
 output carries no autograd history.
 
 The kernels read a packed copy of the parameters. It is rebuilt when a
-parameter's storage, version counter, dtype or device changes. Writes through
-`param.data` (which the reference loader uses) do not move the version counter,
-so call refresh_packed() after such a write, or load with load_tucker() below.
+parameter's storage, version counter, dtype or device changes, or when its
+`.data` has been accessed: the reference loader writes every weight through
+`param.data.copy_(...)` (pure_torch_mlx/weights.py:74-81), which leaves the
+version counter unchanged, so the parameters are TrackedParameter instances
+that count those accesses (any access, read or write, forces one re-pack).
 
 fp8 weights (no counterpart in the reference): load_fp8() or quantize_fp8_()
 switch a bf16 module to U_in, core and U_out held as e4m3 codes with
@@ -38,6 +40,39 @@ from . import _lib
 from . import fp8 as _fp8
 
 
+class TrackedParameter(nn.Parameter):
+    """nn.Parameter that counts accesses to `.data`.
+
+    In-place writes through `param.data` (the reference loader,
+    pure_torch_mlx/weights.py:74-81: `moe.U_in.data.copy_(w[...])`) bypass the
+    parameter's version counter, which is what a cache of derived state usually
+    keys on. Every get or set of `.data` increments `tracked_gen(param)`, which
+    TuckerMoE's packed-weight cache key includes. Behaves as nn.Parameter
+    otherwise (state_dict, load_state_dict, .to(), deepcopy keep the class)."""
+
+    def __new__(cls, data=None, requires_grad=True):
+        return super().__new__(cls, data, requires_grad)
+
+    @property
+    def data(self):
+        self.__dict__["_tmoe_gen"] = self.__dict__.get("_tmoe_gen", 0) + 1
+        return torch.Tensor.data.__get__(self)
+
+    @data.setter
+    def data(self, value):
+        self.__dict__["_tmoe_gen"] = self.__dict__.get("_tmoe_gen", 0) + 1
+        torch.Tensor.data.__set__(self, value)
+
+
+def tracked_gen(p: torch.Tensor) -> int:
+    """Number of `.data` accesses of a TrackedParameter (0 for other tensors)."""
+    return p.__dict__.get("_tmoe_gen", 0)
+
+
+def _tracked(p: nn.Parameter) -> TrackedParameter:
+    return p if isinstance(p, TrackedParameter) else TrackedParameter(p.detach(), p.requires_grad)
+
+
 # state_dict keys of TuckerMoE's parameters, in the order of TuckerMoE._params()
 PARAM_KEYS = ("router.weight", "U_in", "inner_norm.weight", "U_expert", "core", "U_out", "bias")
 
@@ -52,7 +87,7 @@ class RMSNorm(nn.Module):
 
     def __init__(self, dim: int, eps: float = 1e-5):
         super().__init__()
-        self.weight = nn.Parameter(torch.ones(dim))
+        self.weight = TrackedParameter(torch.ones(dim))
         self.eps = eps
 
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -81,12 +116,13 @@ class TuckerMoE(nn.Module):
         r1, r2, r3 = cfg.kmoe_r1, cfg.kmoe_r2, cfg.kmoe_r3
         self.top_k = cfg.kmoe_top_k
         self.router = nn.Linear(d_in, E, bias=False)
-        self.U_in = nn.Parameter(torch.empty(d_in, r3))
+        self.router.weight = _tracked(self.router.weight)
+        self.U_in = TrackedParameter(torch.empty(d_in, r3))
         self.inner_norm = RMSNorm(r3, eps=cfg.rms_norm_eps)
-        self.U_expert = nn.Parameter(torch.empty(E, r1))
-        self.core = nn.Parameter(torch.empty(r1, r3, r2))
-        self.U_out = nn.Parameter(torch.empty(r2, d_out))
-        self.bias = nn.Parameter(torch.zeros(d_out))
+        self.U_expert = TrackedParameter(torch.empty(E, r1))
+        self.core = TrackedParameter(torch.empty(r1, r3, r2))
+        self.U_out = TrackedParameter(torch.empty(r2, d_out))
+        self.bias = TrackedParameter(torch.zeros(d_out))
         self._plan: Optional[_lib.Plan] = None
         self._packed: Optional[torch.Tensor] = None
         self._packed_key = None
@@ -107,7 +143,13 @@ class TuckerMoE(nn.Module):
 
     def _key(self):
         ts = self._params() + (self._fp8_tensors() if self._fp8 is not None else ())
-        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in ts)
+        return tuple((p.data_ptr(), p._version, tracked_gen(p), p.dtype, p.device) for p in ts)
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        # load_state_dict copies in place (moving the version counters); forget the
+        # packed copy regardless
+        self.refresh_packed()
+        return super()._load_from_state_dict(*args, **kwargs)
 
     def plan(self) -> _lib.Plan:
         dtype = self.U_in.dtype
@@ -257,6 +299,13 @@ class TuckerMoE(nn.Module):
         self.refresh_packed()
         self._plan = None
         out = super()._apply(fn, *args, **kwargs)
+        # a conversion that replaced a parameter object keeps it tracked
+        self.router.weight = _tracked(self.router.weight)
+        self.inner_norm.weight = _tracked(self.inner_norm.weight)
+        for name in ("U_in", "U_expert", "core", "U_out", "bias"):
+            p = getattr(self, name)
+            if not isinstance(p, TrackedParameter):
+                setattr(self, name, _tracked(p))
         if self._fp8 is not None:
             # follow the parameters' device; codes and scales keep their dtypes
             dev = self.U_in.device

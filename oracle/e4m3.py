@@ -27,11 +27,15 @@ def decode(codes) -> np.ndarray:
 def dequantize(codes, scale, name: str) -> np.ndarray:
     """float64 weight of `name` from its codes and per-output-channel scales:
     U_in (d_in, r3) with scales (r3,), core (r1, r3, r2) with (r1, r2),
-    U_out (r2, d_out) with (d_out,)."""
+    U_out (r2, d_out) with (d_out,). A channel whose scale is zero is zero,
+    whatever its codes (NaN codes included): the C ABI's fp8 contract (tmoe.h,
+    tmoe_pack_weights_fp8), which a plain decode(q) * s would break for NaN codes."""
     v = decode(codes)
     s = np.asarray(scale, dtype=np.float64)
     if name == "core":
-        return v * s[:, None, :]
-    if name in ("U_in", "U_out"):
-        return v * s[None, :]
-    raise ValueError(f"no fp8 layout for {name!r}")
+        s = s[:, None, :]
+    elif name in ("U_in", "U_out"):
+        s = s[None, :]
+    else:
+        raise ValueError(f"no fp8 layout for {name!r}")
+    return np.where(s == 0, 0.0, v * s)

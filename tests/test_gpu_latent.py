@@ -110,3 +110,37 @@ def test_training_layer_gradients(pkg, dev):
     for (n, p), (_, q) in zip(m.named_parameters(), ref.named_parameters()):
         err = onp.rel_l2(p.grad.cpu().numpy(), q.grad.numpy())
         assert err <= 1e-4, (n, err)
+
+
+def test_latent_fp32_probs_with_bf16_activations(pkg, dev):
+    """bf16 x / G with fp32 top_k_probs: the reference's forward and dG kernels read
+    the probabilities in fp32 (model.py:160-174, :196-219) and its dprobs has their
+    dtype. The GPU result must match the float64 layer with the fp32 probabilities
+    (to the bf16 bar), sit closer to it than to the layer with bf16-rounded ones
+    (the probabilities are not rounded on the way), and dp come back as fp32."""
+    B, E, k, r3, r2 = 2048, 8, 2, 256, 1024
+    x, G, idx, _, dout = _inputs(B, E, k, r3, r2, torch.bfloat16, 77)
+    g = torch.Generator().manual_seed(78)
+    v = torch.randn(B, k, generator=g).sort(-1, descending=True).values
+    p = torch.softmax(v, -1)                        # fp32, not bf16-representable
+    assert not torch.equal(p, p.to(torch.bfloat16).float())
+    xs = x.to(dev).requires_grad_(True)
+    Gs = G.to(dev).requires_grad_(True)
+    ps = p.to(dev).requires_grad_(True)
+    out = pkg.FusedLatentMoE.apply(xs, Gs, idx.to(dev), ps)
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    assert ps.grad.dtype == torch.float32
+    pb = p.to(torch.bfloat16).double()
+    ref32, refb = ln.forward(x, G, idx, p.double()), ln.forward(x, G, idx, pb)
+    dx32, dG32, dp32 = ln.backward(x, G, idx, p.double(), dout)
+    _, dGb, _ = ln.backward(x, G, idx, pb, dout)
+    o = out.detach().float().cpu().numpy()
+    dGg = Gs.grad.float().cpu().numpy()
+    errs = {"out": onp.rel_l2(o, ref32), "dx": onp.rel_l2(xs.grad.float().cpu().numpy(), dx32),
+            "dG": onp.rel_l2(dGg, dG32), "dp": onp.rel_l2(ps.grad.cpu().numpy(), dp32)}
+    print("fp32 probs: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    for n, e in errs.items():
+        assert e <= 1e-2, (n, e)
+    assert onp.rel_l2(o, ref32) < 0.85 * onp.rel_l2(o, refb)
+    assert onp.rel_l2(dGg, dG32) < 0.85 * onp.rel_l2(dGg, dGb)

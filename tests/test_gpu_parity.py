@@ -5,6 +5,8 @@ and <= 1e-2 (bf16) of the reference's PyTorch path. For bf16 workloads the
 reference path is run in float32 on the bf16-valued inputs (fp32 router logits),
 which is oracle/tucker_moe_torch.forward(compute_dtype=float32).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -167,11 +169,41 @@ def test_repack_after_parameter_update(pkg, dev):
     p2 = dict(params)
     p2["bias"] = params["bias"] + 1.0
     assert onp.rel_l2(out.numpy(), onp.forward_f64(x, p2, w.k)["out"]) < 1e-5
-    m.U_out.data.mul_(0.0)    # .data writes need refresh_packed()
-    m.refresh_packed()
+    m.U_out.data.mul_(0.0)    # a .data write: the tracked parameter forces a re-pack
     with torch.no_grad():
         out = m(x.to(dev)).cpu()
     assert torch.allclose(out, p2["bias"].expand_as(out))
+
+
+def _load_tucker_ref_style(moe, w, pfx):
+    """The reference loader's write pattern (pure_torch_mlx/weights.py:74-81):
+    every weight through `param.data.copy_`, no refresh call."""
+    moe.router.weight.data.copy_(w[f"{pfx}.router.weight"])
+    moe.U_in.data.copy_(w[f"{pfx}.U_in"])
+    moe.inner_norm.weight.data.copy_(w[f"{pfx}.inner_norm.weight"])
+    moe.U_expert.data.copy_(w[f"{pfx}.U_expert"])
+    moe.core.data.copy_(w[f"{pfx}.core"])
+    moe.U_out.data.copy_(w[f"{pfx}.U_out"])
+    moe.bias.data.copy_(w[f"{pfx}.bias"])
+
+
+@pytest.mark.parametrize("name,tol", [("C1", 1e-5), ("C2", 1e-2)])
+def test_reference_loader_after_forward(pkg, dev, name, tol):
+    """forward, reload new weights the way the reference loader does, forward
+    again: the second output is the new layer's (no stale packed weights)."""
+    w = pkg.WORKLOADS[name]
+    p1 = pkg.synth.make_params(w, affine="random")
+    p2 = pkg.synth.make_params(dataclasses.replace(w, seed=w.seed + 17), affine="random")
+    x = pkg.synth.make_x(w, 24)
+    m = _module(pkg, dev, w, p1)
+    with torch.no_grad():
+        out1 = m(x.to(dev)).float().cpu()
+        _load_tucker_ref_style(m, {f"L.{k}": v.to(dev, w.dtype) for k, v in p2.items()}, "L")
+        out2, idx2, _, _ = m.forward_with_routing(x.to(dev))
+    r1, r2 = onp.forward_f64(x, p1, w.k), onp.forward_f64(x, p2, w.k)
+    assert onp.rel_l2(out1.numpy(), r1["out"]) < tol
+    assert onp.rel_l2(out2.float().cpu().numpy(), r2["out"]) < tol
+    assert np.array_equal(idx2.cpu().numpy(), r2["idx"])
 
 
 def test_side_stream(pkg, dev):
@@ -252,7 +284,8 @@ def test_fp8_full_size(pkg, dev):
 @pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
 def test_fp8_every_code_and_zero_scales(pkg, dev, T, r1, r2, fold):
     """Every finite e4m3 code appears in each weight, with some channels' scales
-    zero (and, for core, a zero scale between non-zero ones of the same column).
+    zero (and, for core, a zero scale between non-zero ones of the same column);
+    the zero-scaled channels also hold NaN codes, which they must not propagate.
     r1 = 3 with r2 = 320 runs the rank-rescaling core on a partial last tile,
     r1 = 4 with r2 = 256 the persistent core (scales in its epilogue); T = 40 takes
     the small-T kernels, T = 300 the large-tile ones."""
@@ -277,6 +310,12 @@ def test_fp8_every_code_and_zero_scales(pkg, dev, T, r1, r2, fold):
     codes["core_scale"][1, ::5] = 0        # rank 1 of every 5th column: 0 between non-zero
     codes["core_scale"][-1, 3::11] = 0     # the last rank
     codes["U_out_scale"][::13] = 0
+    # NaN codes (0x7F, 0xFF) in zero-scaled channels: a zero scale zeroes its channel
+    codes["U_in_q"][::3, ::7] = 0x7F
+    codes["U_in_q"][1::3, ::7] = 0xFF
+    codes["core_q"][1, ::4, ::5] = 0xFF
+    codes["core_q"][-1, 1::3, 3::11] = 0x7F
+    codes["U_out_q"][::2, ::13] = 0xFF
     params = {k: v.to(torch.bfloat16) for k, v in p32.items()}
     ref = _fp8_reference(params, codes)
     x = pkg.synth.make_x(w)

@@ -128,3 +128,34 @@ def test_fp8_load_validation(pkg):
     m32 = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg())
     with pytest.raises(RuntimeError, match="bfloat16 module"):
         m32.load_fp8(*args)
+
+
+def test_data_writes_invalidate_packed_key(pkg):
+    """The reference loader writes through `param.data.copy_` (weights.py:74-81),
+    which does not move a parameter's version counter: the packed-weight cache key
+    must change anyway, for every parameter."""
+    w = pkg.WORKLOADS["C1"]
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg())
+    m.load_state_dict(pkg.synth.make_params(w))
+    for p in m._params():
+        k0 = m._key()
+        v0 = p._version
+        p.data.copy_(p.detach() * 2)
+        assert p._version == v0            # what made the old key blind to it
+        assert m._key() != k0
+    k0 = m._key()
+    _ = m.state_dict()
+    assert m._key() == k0                  # reading the state does not force a re-pack
+    m._packed, m._packed_key = torch.zeros(1), k0
+    m.load_state_dict(pkg.synth.make_params(w))
+    assert m._packed is None               # load_state_dict forgets the packed copy
+
+
+def test_tracked_parameters_survive_conversion(pkg):
+    import copy
+    w = pkg.WORKLOADS["C1"]
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg())
+    m2 = copy.deepcopy(m).to(torch.float64)
+    for mm in (m, m2):
+        assert all(isinstance(p, pkg.module.TrackedParameter) for p in mm._params())
+    assert m2.U_in.dtype == torch.float64 and set(m2.state_dict()) == set(REF_PARAMS)

@@ -400,3 +400,20 @@ def test_folded_form_identity(d):
     # a transposed core face breaks it
     Wt = np.swapaxes(core, 1, 2).reshape(r1 * r3, r2) @ U_out if r3 == r2 else W[::-1]
     assert onp.rel_l2(A @ Wt + bias, ref["out"].numpy()) > 1e-3
+
+
+def test_e4m3_zero_scale_zeroes_channel():
+    from oracle import e4m3
+    """The fp8 contract (tmoe.h): a zero scale zeroes its channel whatever its
+    codes, NaN codes included; a non-zero scale keeps a NaN code NaN."""
+    q = np.full((3, 4), 0x7F, np.uint8)
+    q[:, 1] = 0xFF
+    s = np.array([0.0, 0.0, 1.0, 0.5])
+    w = e4m3.dequantize(q, s, "U_in")
+    assert np.array_equal(w[:, :2], np.zeros((3, 2)))
+    assert np.isnan(w[:, 2:]).all()
+    qc = np.full((2, 3, 4), 0xFF, np.uint8)
+    sc = np.ones((2, 4))
+    sc[1, 2] = 0.0
+    wc = e4m3.dequantize(qc, sc, "core")
+    assert np.array_equal(wc[1, :, 2], np.zeros(3)) and np.isnan(wc[0]).all()
