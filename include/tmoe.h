@@ -209,6 +209,21 @@ int tmoe_forward_epi(const tmoe_plan* plan, const void* x, int64_t T, const void
                      void* workspace, size_t workspace_bytes, int epi_mode,
                      const void* epi_a, const void* epi_b, void* stream);
 
+/* tmoe_forward without a workspace argument: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): the forward's workspace is a
+ * static device array of tmoe_static_scratch_bytes() bytes (48 MiB: T up to 16384
+ * at the reference's C3 shape) that each GPU the library runs on holds until the
+ * process ends; this call allocates nothing. T whose workspace
+ * (tmoe_workspace_bytes) exceeds it gives TMOE_EUNSUPPORTED before any GPU work.
+ * All calls on one GPU share that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from different threads without ordering) race. Arguments,
+ * results and errors otherwise as tmoe_forward; not recorded by tmoe_prof_*. */
+size_t tmoe_static_scratch_bytes(void);
+int tmoe_forward_static(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
+                        void* out, int32_t* topk_idx, float* topk_w, float* logits,
+                        void* stream);
+
 /* out = R(R(silu(gate(x))) * up(x)) for two layers of one plan over the same input:
  * F.silu(ffn_gate(x_f)) * ffn_up(x_f) of model.py:338-340, i.e. tmoe_forward of the
  * gate's packed weights into `out` followed by tmoe_forward_epi(TMOE_EPI_GLU, out) of

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libtmoe.so")
 
-SOURCES = ["tmoe_kernels.hip", "tmoe_api.cpp"]
+SOURCES = ["tmoe_kernels.hip", "tmoe_static.hip", "tmoe_api.cpp"]
 ARCH = "gfx950"
 
 # Packed FP32 vector instructions are disabled for all device code: hipcc -O3

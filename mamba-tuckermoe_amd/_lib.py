@@ -36,6 +36,7 @@ EXPORTED = (
     "tmoe_plan_core_rank", "tmoe_plan_folded",
     "tmoe_pack_weights", "tmoe_pack_weights_fp8",
     "tmoe_forward", "tmoe_forward_epi", "tmoe_forward_glu", "tmoe_rmsnorm_rows",
+    "tmoe_static_scratch_bytes", "tmoe_forward_static",
     "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
@@ -107,6 +108,10 @@ def lib() -> ctypes.CDLL:
         L.tmoe_forward_epi.restype = ctypes.c_int
         L.tmoe_forward_epi.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, ctypes.c_int,
                                        vp, vp, vp]
+        L.tmoe_static_scratch_bytes.restype = sz
+        L.tmoe_static_scratch_bytes.argtypes = []
+        L.tmoe_forward_static.restype = ctypes.c_int
+        L.tmoe_forward_static.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp]
         L.tmoe_forward_glu.restype = ctypes.c_int
         L.tmoe_forward_glu.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, sz, vp]
         L.tmoe_rmsnorm_rows.restype = ctypes.c_int

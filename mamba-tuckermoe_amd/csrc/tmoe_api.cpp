@@ -447,11 +447,13 @@ int tmoe_forward(const tmoe_plan* p, const void* x, int64_t T, const void* packe
                           workspace_bytes, TMOE_EPI_NONE, nullptr, nullptr, stream);
 }
 
-int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
-                     int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
-                     size_t workspace_bytes, int epi_mode, const void* epi_a, const void* epi_b,
-                     void* stream) {
-  g_err[0] = 0;
+namespace {
+// The forward of tmoe_forward_epi (argument checks included). With prof_ok false
+// no profiling event is recorded (tmoe_forward_static).
+int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
+                 int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
+                 size_t workspace_bytes, int epi_mode, const void* epi_a, const void* epi_b,
+                 void* stream, bool prof_ok) {
   if (!p) return fail(TMOE_EINVAL, "tmoe_forward: null plan");
   if (epi_mode != TMOE_EPI_NONE && epi_mode != TMOE_EPI_GLU && epi_mode != TMOE_EPI_RESIDUAL_SCALE)
     return fail(TMOE_EINVAL, "tmoe_forward_epi: epi_mode %d is not a TMOE_EPI_* value", epi_mode);
@@ -494,7 +496,7 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
 
   std::vector<hipEvent_t> ev;
   std::unique_lock<std::mutex> lk(g_prof.mu);
-  const bool prof = g_prof.on;
+  const bool prof = g_prof.on && prof_ok;
   if (!prof) lk.unlock();
   // on an error the events taken so far go back to the pool (the lock is held)
   auto release = [&](hipEvent_t extra) {
@@ -527,6 +529,44 @@ int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* p
     g_prof.pending.push_back(std::move(ev));
   }
   return TMOE_OK;
+}
+}  // namespace
+
+int tmoe_forward_epi(const tmoe_plan* p, const void* x, int64_t T, const void* packed, void* out,
+                     int32_t* topk_idx, float* topk_w, float* logits, void* workspace,
+                     size_t workspace_bytes, int epi_mode, const void* epi_a, const void* epi_b,
+                     void* stream) {
+  g_err[0] = 0;
+  return forward_impl(p, x, T, packed, out, topk_idx, topk_w, logits, workspace, workspace_bytes,
+                      epi_mode, epi_a, epi_b, stream, true);
+}
+
+size_t tmoe_static_scratch_bytes(void) { return tmoe::kStaticScratchBytes; }
+
+int tmoe_forward_static(const tmoe_plan* p, const void* x, int64_t T, const void* packed,
+                        void* out, int32_t* topk_idx, float* topk_w, float* logits,
+                        void* stream) {
+  g_err[0] = 0;
+  if (!p) return fail(TMOE_EINVAL, "tmoe_forward_static: null plan");
+  if (T < 0) return fail(TMOE_EINVAL, "tmoe_forward_static: T=%lld < 0", (long long)T);
+  if (T > (int64_t)1 << 30)
+    return fail(TMOE_EUNSUPPORTED, "tmoe_forward_static: T=%lld too large", (long long)T);
+  if (T == 0) return TMOE_OK;
+  // every check that needs no GPU comes before the scratch lookup
+  const size_t need = workspace_layout(p, T).total;
+  if (need > tmoe::kStaticScratchBytes)
+    return fail(TMOE_EUNSUPPORTED,
+                "tmoe_forward_static: T=%lld needs %zu bytes of scratch, more than the static "
+                "maximum of %zu (use tmoe_forward with a workspace, or fewer tokens per call)",
+                (long long)T, need, tmoe::kStaticScratchBytes);
+  if (!x || !packed || !out) return fail(TMOE_EINVAL, "tmoe_forward_static: null x/packed/out");
+  if (!aligned16(x) || !aligned16(packed) || !aligned16(out))
+    return fail(TMOE_EINVAL, "tmoe_forward_static: x/packed/out must be 16-byte aligned");
+  void* ws = nullptr;
+  if (hipError_t e = tmoe::static_scratch(&ws); e != hipSuccess)
+    return hip_fail(e, "tmoe_forward_static: static scratch address");
+  return forward_impl(p, x, T, packed, out, topk_idx, topk_w, logits, ws,
+                      tmoe::kStaticScratchBytes, TMOE_EPI_NONE, nullptr, nullptr, stream, false);
 }
 
 int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* packed_gate,

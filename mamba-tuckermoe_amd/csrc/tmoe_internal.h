@@ -11,6 +11,12 @@ namespace tmoe {
 // the kernels. K-direction tiles are 128 bytes of one operand row: 64 bf16 or
 // 32 f32 elements.
 constexpr int kTileKBytes = 128;
+// Bytes of the static scratch of tmoe_forward_static (tmoe_static.hip): the
+// forward's workspace for up to T = 16384 tokens at the reference's C3 shape.
+constexpr size_t kStaticScratchBytes = (size_t)48 << 20;
+// Device address of the static scratch on the current GPU (looked up once per GPU).
+hipError_t static_scratch(void** ptr);
+
 constexpr int kFrontBM = 64;    // tokens per k_front work-group (whole r3 and E rows)
 constexpr int kFrontPFA = 8;    // K tiles of x in flight per k_front work-group
 constexpr int kFrontWM = 2;     // row groups of waves per k_front work-group

@@ -279,3 +279,24 @@ def test_plan_folded(pkg, kw, folded):
     finally:
         L.tmoe_plan_destroy(p)
     assert L.tmoe_plan_folded(None) == 0
+
+
+def test_forward_static_rejects_before_gpu_work(pkg):
+    """tmoe_forward_static: every size and pointer check happens on the host before
+    the static scratch is looked up (no GPU needed for these paths)."""
+    L = pkg._lib.lib()
+    assert L.tmoe_static_scratch_bytes() == 48 << 20
+    rc, p, msg = _create(pkg, d_in=1536, d_out=2304, E=16, k=2, r1=4, r2=1024, r3=256, dtype=BF16)
+    assert rc == 0, msg
+    try:
+        assert L.tmoe_forward_static(None, 16, 4, 16, 16, None, None, None, None) == -1
+        assert L.tmoe_forward_static(p, 16, 0, 16, 16, None, None, None, None) == 0   # T = 0
+        assert L.tmoe_forward_static(p, 16, -1, 16, 16, None, None, None, None) == -1
+        # the C3 shape: 16384 tokens fit, twice that does not
+        assert L.tmoe_workspace_bytes(p, 16384) <= L.tmoe_static_scratch_bytes()
+        rc = L.tmoe_forward_static(p, 16, 32768, 16, 16, None, None, None, None)
+        assert rc == -2 and b"static maximum" in L.tmoe_last_error()
+        assert L.tmoe_forward_static(p, None, 64, 16, 16, None, None, None, None) == -1
+        assert L.tmoe_forward_static(p, 8, 64, 16, 16, None, None, None, None) == -1  # misaligned
+    finally:
+        L.tmoe_plan_destroy(p)
