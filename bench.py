@@ -47,18 +47,26 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def traffic_per_launch(workload: str, kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary
-    (profiles/tmoe_forward_<workload>_traffic.md, line 'traffic_bytes <kernel> <bytes>'),
-    or None when it has not been measured."""
-    path = os.path.join(ROOT, "profiles", f"tmoe_forward_{workload}_traffic.md")
-    if not os.path.exists(path):
-        return None
-    for line in open(path):
-        f = line.strip().strip("`").split()
-        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
-            return float(f[2])
+def profile_figure(workload: str, key: str, stage: str):
+    """A per-launch figure of `stage` from the committed rocprofv3 counter summaries
+    (profiles/tmoe_forward_<workload>_counters.md, then ..._traffic.md; a line
+    '<key> <stage> <value>'), or None when it has not been measured.
+    key 'traffic_bytes': FETCH_SIZE + WRITE_SIZE bytes, calibrated against a copy;
+    key 'mfma_util': SQ_VALU_MFMA_BUSY_CYCLES over the GPU-active cycles x SIMDs."""
+    for name in (f"tmoe_forward_{workload}_counters.md", f"tmoe_forward_{workload}_traffic.md"):
+        path = os.path.join(ROOT, "profiles", name)
+        if not os.path.exists(path):
+            continue
+        for line in open(path):
+            f = line.strip().strip("`").split()
+            if len(f) == 3 and f[0] == key and f[1] == stage:
+                return float(f[2])
     return None
+
+
+def traffic_per_launch(workload: str, kernel: str):
+    """HBM bytes per launch of stage `kernel` (see profile_figure)."""
+    return profile_figure(workload, "traffic_bytes", kernel)
 
 
 def cpu_threads():
@@ -445,8 +453,13 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: 3 x {args.copy_calibration_mib} MiB device copies")
 
+    full_size = T == pkg.WORKLOADS[w.name].T
     traffic = (traffic_per_launch(w.name, dom + ("_folded" if folded else ""))
-               if T == pkg.WORKLOADS[w.name].T else None)
+               if full_size else None)
+    # MFMA-busy share of the dominant stage from the committed counter pass (the
+    # timing-derived share is `frac`: executed flops / avg duration / peak at 2.4 GHz)
+    mfma_util = (profile_figure(w.name, "mfma_util", dom + "_folded")
+                 if full_size and folded else None)
 
     # -- parity on a slice (GPU result of set 0 vs the fp32 reference path) --------
     from oracle import tucker_moe_np as onp
@@ -504,10 +517,14 @@ def main():
                    "form": form},
         "roofline": ({"bound": "mfma", "kernel": dom, "achieved": dom_tflops, "peak": peak,
                       "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
+                      "mfma_util_counter": mfma_util,
+                      "mfma_util_source": (f"profiles/tmoe_forward_{w.name}_counters.md"
+                                           if mfma_util is not None else None),
                       "avg_us": stage_avg_us[dom], "flops_per_launch": fl[dom]}
                      if mfma_bound else
                      {"bound": "hbm", "kernel": dom, "achieved": dom_gbs, "peak": HBM_PEAK_GBS,
                       "unit": "GB/s", "frac": dom_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                      "mfma_util_counter": mfma_util,
                       "avg_us": stage_avg_us[dom], "bytes_per_launch": sb[dom]}),
         "layer": {"tflops": layer_tflops, "mfma_frac": layer_tflops / peak,
                   "flops_per_step": fl_algo["total"],
