@@ -55,6 +55,7 @@ struct FwdArgs {
   float* c;                     // (T, r1)
   void* z;                      // (T, r3)
   void* mid;                    // (T, r2); folded plans: c (x) z (T, r1*r3)
+  bool mid_rows_256;            // mid is allocated for T rounded up to 256 rows
   void* cz;                     // folded plans whose front writes c (x) z itself (= mid;
                                 //                      then z is not stored), else null
   float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]

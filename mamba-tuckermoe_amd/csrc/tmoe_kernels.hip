@@ -4,6 +4,7 @@
 #include "tmoe_kernels.hpp"
 #include "tmoe_small.hpp"
 #include "tmoe_latent.hpp"
+#include "tmoe_outproj_wide.hpp"
 
 namespace tmoe {
 namespace {
@@ -171,12 +172,31 @@ int cu_count() {
   return n;
 }
 
+// k_outproj_wide's contract: bf16, no column scale, no fused epilogue, K a
+// multiple of 64, whole 288-column tiles, A (mid) allocated for T rounded up to
+// 256 rows (the workspace rounds its tile rows to 256 for these plans), and at
+// least one tile per compute unit (fewer leave units idle, where k_outproj_pp's
+// smaller tiles do better).
+bool outproj_wide_ok(const FwdArgs& a, int64_t ncu) {
+  if (a.dtype != kDtypeBF16 || a.out_scale || a.epi_mode != kEpiNone) return false;
+  if (a.r2 % 64 != 0 || a.d_out % dev::wide::BN != 0 || !a.mid_rows_256) return false;
+  return cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN) >= ncu;
+}
+
 // bf16 out-projection: persistent, one work-group per compute unit (its LDS
 // holds one), each looping over the tiles b, b + grid, ...
 hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
   typedef OutCfgBF16 C;
-  const int64_t tiles = (int64_t)cdiv(a.T, C::BM) * cdiv(a.d_out, C::BN);
   const int64_t ncu = cu_count();
+  if (outproj_wide_ok(a, ncu)) {
+    const int64_t wt = cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN);
+    const dim3 grid((unsigned)(wt < ncu ? wt : ncu)), block(256);
+    hipLaunchKernelGGL(dev::k_outproj_wide, grid, block, 0, st,
+                       static_cast<const uint16_t*>(a.mid), static_cast<const uint16_t*>(a.uoutT),
+                       static_cast<uint16_t*>(a.out), a.bias, (int)a.T, (int)a.d_out, (int)a.r2);
+    return hipGetLastError();
+  }
+  const int64_t tiles = (int64_t)cdiv(a.T, C::BM) * cdiv(a.d_out, C::BN);
   if (2 * tiles <= ncu) {
     // at most half the compute units busy: tiles of 128 tokens, twice as many
     const int64_t t128 = (int64_t)cdiv(a.T, 128) * cdiv(a.d_out, C::BN);

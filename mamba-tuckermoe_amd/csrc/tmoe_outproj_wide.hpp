@@ -1,0 +1,287 @@
+// The large-T bf16 out-projection out = A W^T + bias as a persistent GEMM with
+// 256 x 288 output tiles (reference: model.py:101's `core @ self.U_out + bias`,
+// here with A = mid or, for folded plans, c (x) z, and W^T = U_out^T or
+// (core U_out)^T).
+//
+// One work-group of 4 waves per compute unit, one wave per SIMD. A wave owns 64
+// rows x 288 columns: 18 accumulator blocks of 32 x 32, 16 of them pinned to the
+// AGPRs and 2 to VGPRs through inline-asm MFMAs (builtin MFMAs on this many
+// accumulators made the compiler copy them between the register files around
+// every MFMA). K tiles of 64 (128 bytes of a row) stream by DMA into two LDS
+// stages of 544 rows (256 of A, 288 of W^T) with the swizzle of lds_slot.
+//
+// The epilogue stores come from the accumulators directly (lanes l and l + 32
+// swap halves with v_permlane32_swap so that each lane writes 16 contiguous
+// bytes). On gfx9 one counter (vmcnt) covers loads and stores in issue order,
+// so a wait for a DMA issued after a burst of stores also waits for the
+// stores. The next tile's first two K tiles are therefore issued before the
+// stores, and the waits that follow leave the stores outstanding: they drain
+// under the next tile's first K tiles. The bias columns come through the
+// scalar unit (no LDS read after the DMA, which would wait for it).
+//
+// Shape contract (checked by the host): K % 64 == 0, N % 288 == 0 (W^T rows
+// read in whole tiles), A allocated for T rounded up to 256 rows (rows past T
+// are read, their results never stored), no column scale and no fused
+// epilogue.
+#pragma once
+
+namespace tmoe {
+namespace dev {
+
+namespace wide {
+
+constexpr int BM = 256;          // tokens per tile
+constexpr int FN = 9;            // 32-column blocks per tile
+constexpr int BN = 32 * FN;      // 288 columns
+constexpr int FM = 2;            // 32-row blocks per wave (64 rows)
+constexpr int kAgprBlk = 16;     // accumulator blocks in AGPRs; the rest in VGPRs
+constexpr int kRows = BM + BN;   // operand rows per K tile
+constexpr int kStage = kRows * 8;       // 16-byte slots per stage
+constexpr int kBlocks = kRows / 8;      // 8-row DMA blocks per stage
+constexpr int kDmaPerWave = kBlocks / 4;
+constexpr int kABlocksPerWave = BM / 32;
+constexpr int kStores = 2 * FN * FM;    // epilogue stores per wave of a full tile
+static_assert(kBlocks % 4 == 0, "DMA blocks split evenly over 4 waves");
+static_assert(kDmaPerWave + kStores <= 63, "counted waits within the vmcnt range");
+
+}  // namespace wide
+
+#define TMOE_MFMA_A(acc, b, a) \
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(b), "v"(a))
+#define TMOE_MFMA_V(acc, b, a) \
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(b), "v"(a))
+#define TMOE_MFMA_A0(acc, b, a) \
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(b), "v"(a))
+#define TMOE_MFMA_V0(acc, b, a) \
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(b), "v"(a))
+
+// One K step (16 of K) of a wave's 18 blocks, W^T fragment first (transposed
+// result: lane l holds row l & 31 of the block and columns 8 q + 4 (l >> 5) +
+// 0..3 in elements 4 q .. 4 q + 3). ld(b) runs after the b-th MFMA: the next
+// step's fragment reads, spread between the MFMAs.
+template <bool kZero, class LD>
+__device__ __forceinline__ void wide_step(f32x16 (&acc)[wide::FM][wide::FN],
+                                          const u32x4 (&af)[wide::FM],
+                                          const u32x4 (&bf)[wide::FN], LD&& ld) {
+#pragma unroll
+  for (int j = 0; j < wide::FN; ++j)
+#pragma unroll
+    for (int i = 0; i < wide::FM; ++i) {
+      const int blk = j * wide::FM + i;
+      if (kZero) {
+        if (blk < wide::kAgprBlk) TMOE_MFMA_A0(acc[i][j], bf[j], af[i]);
+        else TMOE_MFMA_V0(acc[i][j], bf[j], af[i]);
+      } else {
+        if (blk < wide::kAgprBlk) TMOE_MFMA_A(acc[i][j], bf[j], af[i]);
+        else TMOE_MFMA_V(acc[i][j], bf[j], af[i]);
+      }
+      ld(blk);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32. The pointers
+// are separate restrict parameters: that lets the compiler read bias through
+// the scalar unit (it may assume no store of C clobbers it).
+__global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict__ A,
+                                                      const uint16_t* __restrict__ Bt,
+                                                      uint16_t* __restrict__ C,
+                                                      const float* __restrict__ bias, int M,
+                                                      int N, int K) {
+  using namespace wide;
+  __shared__ u32x4 smem[2 * kStage];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ntn = N / BN;
+  const int ntiles = ((M + BM - 1) / BM) * ntn;
+  const int nkt = K / 64;
+  const uint32_t row_bytes = (uint32_t)K * 2;
+
+  f32x16 acc[FM][FN];
+  u32x4 fa[2][FM], fb[2][FN];
+
+  int t = blockIdx.x;
+  if (t >= ntiles) return;
+  int tm, tn;
+  tile_coords_of(t, ntn, ntiles, tm, tn);
+
+  // DMA block wave + 4 d of a stage: A rows 32 d + 8 wave + (lane >> 3) for
+  // d < kABlocksPerWave, else W^T rows 32 (d - kABlocksPerWave) + 8 wave +
+  // (lane >> 3). Whole tiles are in bounds, so one per-lane offset serves all.
+  const uint32_t voff = (uint32_t)(8 * wave + (lane >> 3)) * row_bytes +
+                        (uint32_t)dma_chunk(lane, wave) * 16u;
+  auto dma = [&](int d, int kt, int stage, int tm_, int tn_) __attribute__((always_inline)) {
+    const char* base;
+    if (d < kABlocksPerWave)
+      base = reinterpret_cast<const char*>(A) + (int64_t)tm_ * BM * row_bytes +
+             (int64_t)d * 32 * row_bytes;
+    else
+      base = reinterpret_cast<const char*>(Bt) + (int64_t)tn_ * BN * row_bytes +
+             (int64_t)(d - kABlocksPerWave) * 32 * row_bytes;
+    base += kt * kTileKBytes;
+    // the LDS address goes through an integer, as in the measured build of this
+    // loop (a pointer with provenance changes the compiler's DMA alias tracking)
+    const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) u32x4*)(
+        smem + stage * kStage + (wave + 4 * d) * 64);
+    __builtin_amdgcn_global_load_lds((gbl_cvptr)(base + voff), (lds_vptr)(size_t)lds, 16, 0, 0);
+  };
+  auto read_frag = [&](int kt, int ks, int buf, int m) __attribute__((always_inline)) {
+    const u32x4* s = smem + (kt & 1) * kStage;
+    const int ch = ks * 2 + (lane >> 5);
+    if (m < FM) fa[buf][m] = s[lds_slot(wave * 64 + m * 32 + (lane & 31), ch)];
+    else if (m < FM + FN) fb[buf][m - FM] = s[lds_slot(BM + (m - FM) * 32 + (lane & 31), ch)];
+  };
+  auto read_frags = [&](int kt, int ks, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < FM + FN; ++m) read_frag(kt, ks, buf, m);
+  };
+
+  // One K tile: the MFMAs of its 4 K steps from fragments read one step ahead;
+  // the DMA of tile kt + 1 (unless issued earlier) over steps 0-1; wait +
+  // barrier after step 2, then the first fragments of tile kt + 1 are read
+  // under step 3's MFMAs. keep_stores: the wait leaves the previous tile's
+  // kStores stores outstanding (issued after this tile's K tile 1 DMA).
+  auto ktile = [&](int kt, bool first, bool more, bool issue, bool keep_stores)
+                   __attribute__((always_inline)) {
+    if (more && issue) {
+#pragma unroll
+      for (int d = 0; d < kDmaPerWave / 2; ++d) dma(d, kt + 1, (kt + 1) & 1, tm, tn);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      auto ld = [&](int m) __attribute__((always_inline)) { read_frag(kt, 1, 1, m); };
+      if (first) wide_step<true>(acc, fa[0], fb[0], ld);
+      else wide_step<false>(acc, fa[0], fb[0], ld);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (more && issue) {
+#pragma unroll
+      for (int d = kDmaPerWave / 2; d < kDmaPerWave; ++d) dma(d, kt + 1, (kt + 1) & 1, tm, tn);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wide_step<false>(acc, fa[1], fb[1],
+                     [&](int m) __attribute__((always_inline)) { read_frag(kt, 2, 0, m); });
+    __builtin_amdgcn_sched_barrier(0);
+    wide_step<false>(acc, fa[0], fb[0],
+                     [&](int m) __attribute__((always_inline)) { read_frag(kt, 3, 1, m); });
+    __builtin_amdgcn_sched_barrier(0);
+    if (keep_stores) wait_vm_lds<kStores>();
+    else wait_vm_lds<0>();
+    lds_barrier();
+    wide_step<false>(acc, fa[1], fb[1], [&](int m) __attribute__((always_inline)) {
+      if (more) read_frag(kt + 1, 0, 0, m);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    // after a tile's last MFMA its accumulator writes land before the registers
+    // are read
+    if (!more) mfma_drain();
+  };
+
+  // prologue of the first tile
+#pragma unroll
+  for (int d = 0; d < kDmaPerWave; ++d) dma(d, 0, 0, tm, tn);
+  wait_vm_lds<0>();
+  lds_barrier();
+  read_frags(0, 0, 0);
+
+  bool pre = false;        // K tile 1 of this tile went out before the previous stores
+  bool pre_full = false;   // ... and all kStores of those stores were issued
+  for (;;) {
+    ktile(0, true, nkt > 1, !pre, pre && pre_full);
+    for (int kt = 1; kt + 1 < nkt; ++kt) ktile(kt, false, true, true, false);
+    if (nkt > 1) ktile(nkt - 1, false, false, true, false);
+    // the next tile's first two K tiles into stages 0 and 1 (both free: every
+    // read of them completed before the last barrier), ahead of the stores
+    const int t_next = t + (int)gridDim.x;
+    const bool has_next = t_next < ntiles;
+    const bool early = has_next && nkt > 1;
+    int tm2 = tm, tn2 = tn;
+    if (has_next) {
+      tile_coords_of(t_next, ntn, ntiles, tm2, tn2);
+#pragma unroll
+      for (int d = 0; d < kDmaPerWave; ++d) dma(d, 0, 0, tm2, tn2);
+      if (early) {
+#pragma unroll
+        for (int d = 0; d < kDmaPerWave; ++d) dma(d, 1, 1, tm2, tn2);
+      }
+    }
+    const bool full = (tm + 1) * BM <= M;
+    {
+      // lane-derived values are recomputed here rather than kept live through
+      // the main loop
+      int ln = threadIdx.x & 63;
+      asm volatile("" : "+v"(ln));
+      const int n0 = tn * BN;
+      const int m0 = tm * BM + wave * 64;
+      const bool hi = ln >= 32;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        // the block's 32 bias values: uniform loads
+        float bj[32];
+        {
+          const float4* bp = reinterpret_cast<const float4*>(bias + n0 + j * 32);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const float4 v = bp[c];
+            bj[4 * c] = v.x; bj[4 * c + 1] = v.y; bj[4 * c + 2] = v.z; bj[4 * c + 3] = v.w;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int row = m0 + i * 32 + (ln & 31);
+          uint32_t pk[4][2];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (j * FM + i < kAgprBlk)   // read the AGPR here, not all at the loop exit
+                asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][4 * q + e]));
+              else
+                v[e] = acc[i][j][4 * q + e];
+              v[e] += hi ? bj[8 * q + 4 + e] : bj[8 * q + e];
+            }
+            pk[q][0] = pack_bf16x2(v[0], v[1]);
+            pk[q][1] = pack_bf16x2(v[2], v[3]);
+          }
+          if (row < M) {
+            // lanes l and l + 32 swap halves: lane l then holds columns 16 p + 0..7
+            // and lane l + 32 columns 16 p + 8..15 of the block
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const auto sx = __builtin_amdgcn_permlane32_swap(pk[2 * p][0], pk[2 * p + 1][0],
+                                                                false, false);
+              const auto sy = __builtin_amdgcn_permlane32_swap(pk[2 * p][1], pk[2 * p + 1][1],
+                                                                false, false);
+              const u32x4 val = {sx[0], sy[0], sx[1], sy[1]};
+              const int col = n0 + j * 32 + 16 * p + 8 * (ln >> 5);
+              *reinterpret_cast<u32x4*>(C + (int64_t)row * N + col) = val;
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (!has_next) break;
+    t = t_next;
+    tm = tm2;
+    tn = tn2;
+    // K tile 0 has landed once at most the DMAs of K tile 1 and the stores remain
+    // (all kStores of them only for a full tile; else the stores are waited for too)
+    if (early && full) wait_vm_lds<kDmaPerWave + kStores>();
+    else if (early) wait_vm_lds<kDmaPerWave>();
+    else wait_vm_lds<0>();
+    lds_barrier();
+    read_frags(0, 0, 0);
+    pre = early;
+    pre_full = full;
+  }
+}
+
+#undef TMOE_MFMA_A
+#undef TMOE_MFMA_V
+#undef TMOE_MFMA_A0
+#undef TMOE_MFMA_V0
+
+}  // namespace dev
+}  // namespace tmoe

@@ -87,6 +87,30 @@ def test_full_size(pkg, dev, name, fold):
     _check(w, got, ref64, f"{name}/full/fold={fold}", tref)
 
 
+# The 256 x 288-tile out-projection (k_outproj_wide) runs when its tiles number at
+# least one per compute unit: a ragged last row tile (whose stores the next tile
+# waits for in full), d_out = 2 column tiles, and both forms.
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+@pytest.mark.parametrize("T", [12345, 16284])
+def test_wide_outproj_ragged(pkg, dev, T, fold):
+    w = pkg.WORKLOADS["C3"]
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, T, stream=5)
+    m = _module(pkg, dev, w, params, fold)
+    got = _run(m, x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"C3/T={T}/fold={fold}")
+
+
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+def test_wide_outproj_narrow(pkg, dev, fold):
+    # (E, k, r1, r3, r2, d_in, d_out): K = 256 either way, 2 column tiles of 288
+    w = pkg.Workload("custom", 32768 - 200, 256, 576, 8, 2, 2, 128, 256, torch.bfloat16, 78)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    got = _run(_module(pkg, dev, w, params, fold), x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"narrow/fold={fold}")
+
+
 @pytest.mark.parametrize("T", [1, 3, 63, 65, 255, 257, 1000])
 @pytest.mark.parametrize("name", ["C1", "C2"])
 def test_ragged_tokens(pkg, dev, name, T):
