@@ -189,6 +189,23 @@ tmoe::FwdArgs folded_args(const tmoe_plan* p, const tmoe::FwdArgs& a, const void
 
 hipError_t launch_nothing(const tmoe::FwdArgs&, hipStream_t) { return hipSuccess; }
 
+using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
+
+// The small-T stages (front, core, out-projection) of a forward with args a: the
+// front epilogue runs inside the core (or, folded, the out-projection) when that
+// kernel's LDS holds it, else as its own kernel after the front's GEMM.
+void small_stages(const tmoe::FwdArgs& a, bool fold, Launch (&st)[kStages]) {
+  if (tmoe::small_epi_fused_ok(a)) {
+    st[0] = tmoe::launch_small_front_raw;
+    st[1] = fold ? launch_nothing : tmoe::launch_small_core_epi;
+    st[2] = fold ? tmoe::launch_small_out_epi : tmoe::launch_small_out;
+  } else {
+    st[0] = tmoe::launch_small_front;
+    st[1] = fold ? launch_nothing : tmoe::launch_small_core;
+    st[2] = fold ? tmoe::launch_small_out_kr : tmoe::launch_small_out;
+  }
+}
+
 // stage 2 of a folded plan: c (x) z, unless the front already wrote it
 hipError_t launch_cz(const tmoe::FwdArgs& f, hipStream_t st) {
   return f.cz ? hipSuccess : tmoe::launch_expand_cz(f, st);
@@ -482,7 +499,6 @@ int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.epi_b = epi_mode == TMOE_EPI_RESIDUAL_SCALE ? epi_b : nullptr;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
   const bool small = T <= tmoe::kSmallT;
   const bool fold = p->fold;
   if (fold) a = folded_args(p, a, packed);
@@ -490,9 +506,8 @@ int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packe
                                     fold ? launch_cz : tmoe::launch_core,
                                     tmoe::launch_outproj};
   // folded: the out-projection builds c (x) z from z and c itself (no core stage)
-  const Launch small_path[kStages] = {tmoe::launch_small_front,
-                                      fold ? launch_nothing : tmoe::launch_small_core,
-                                      fold ? tmoe::launch_small_out_kr : tmoe::launch_small_out};
+  Launch small_path[kStages];
+  small_stages(a, fold, small_path);
   const Launch* stages = small ? small_path : big_path;
   const char* stage_names[kStages] = {"front (router + in-projection)", "core",
                                       "out-projection"};
@@ -597,18 +612,17 @@ int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* p
   u.epi_a = out;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
-  using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
   if (p->fold) {
     g = folded_args(p, g, packed_gate);
     u = folded_args(p, u, packed_up);
   }
   if (T <= tmoe::kSmallT) {
-    const Launch small[kStages] = {
-        tmoe::launch_small_front, p->fold ? launch_nothing : tmoe::launch_small_core,
-        p->fold ? tmoe::launch_small_out_kr : tmoe::launch_small_out};
-    for (const tmoe::FwdArgs* a : {&g, &u})
+    for (const tmoe::FwdArgs* a : {&g, &u}) {
+      Launch small[kStages];
+      small_stages(*a, p->fold, small);
       for (int i = 0; i < kStages; ++i)
         if ((e = small[i](*a, st)) != hipSuccess) return hip_fail(e, "tmoe_forward_glu");
+    }
     return TMOE_OK;
   }
   const Launch mid = p->fold ? launch_cz : tmoe::launch_core;

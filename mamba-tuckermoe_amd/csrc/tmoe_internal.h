@@ -162,6 +162,14 @@ hipError_t launch_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t stream);
 hipError_t launch_core(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_outproj(const FwdArgs& a, hipStream_t stream);
+// Small-T path with the front epilogue fused into the next GEMM (3 launches for
+// unfolded plans, 2 for folded): k_sk_front only, then the core or the folded
+// out-projection, each of whose work-groups runs the epilogue of its tokens.
+// small_epi_fused_ok: the fused kernel's LDS fits (else the separate epilogue).
+hipError_t launch_small_front_raw(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_small_core_epi(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_small_out_epi(const FwdArgs& a, hipStream_t stream);
+bool small_epi_fused_ok(const FwdArgs& a);
 // folded plans (T > kSmallT): mid (T, r1*r3) = c (x) z, the Khatri-Rao row product
 // mid[t, r*r3 + s] = c[t, r] z[t, s] rounded to bf16; launch_outproj then runs with
 // r2 := r1 * r3 and uoutT := W^T

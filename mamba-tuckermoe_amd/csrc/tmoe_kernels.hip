@@ -253,7 +253,28 @@ hipError_t launch_small_out_t(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// the small-T front's GEMM alone (raw), for a consumer that runs the epilogue
+template <int MF, class Elt>
+hipError_t launch_small_front_raw_t(const FwdArgs& a, hipStream_t st) {
+  const dim3 grid(cdiv(a.r3 + a.E, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
+  hipLaunchKernelGGL((dev::k_sk_front<Elt, MF, kSkW>), grid, block, 0, st, a, a.raw);
+  return hipGetLastError();
+}
+
+// the front epilogue fused into the following Khatri-Rao GEMM (core, or the
+// folded out-projection)
+template <int MF, class Elt, bool kCore>
+hipError_t launch_small_epi_gemm_t(const FwdArgs& a, hipStream_t st) {
+  const int64_t N = kCore ? a.r2 : a.d_out;
+  const dim3 grid(cdiv(N, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
+  hipLaunchKernelGGL((dev::k_sk_epi_gemm<Elt, MF, kSkW, kCore>), grid, block,
+                     dev::sk_epi_dyn_bytes(MF, a), st, a);
+  return hipGetLastError();
+}
+
 // rows per work-group: 16, 32 or 64 tokens
+inline int small_mf(int64_t T) { return T <= 16 ? 1 : T <= 32 ? 2 : 4; }
+
 template <template <int, class> class L>
 hipError_t by_rows(const FwdArgs& a, hipStream_t st) {
   const bool bf = a.dtype == kDtypeBF16;
@@ -274,6 +295,21 @@ struct SmallOut {
   static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_out_t<MF, Elt>(a, st); }
 };
 template <int MF, class Elt>
+struct SmallFrontRaw {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_front_raw_t<MF, Elt>(a, st); }
+};
+template <int MF, class Elt>
+struct SmallCoreEpi {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) { return launch_small_epi_gemm_t<MF, Elt, true>(a, st); }
+};
+template <int MF, class Elt>
+struct SmallOutEpi {
+  static hipError_t run(const FwdArgs& a, hipStream_t st) {
+    if constexpr (std::is_same<Elt, EltBF16>::value) return launch_small_epi_gemm_t<MF, Elt, false>(a, st);
+    return hipErrorInvalidValue;   // folded plans are bf16
+  }
+};
+template <int MF, class Elt>
 struct SmallOutKR {
   static hipError_t run(const FwdArgs& a, hipStream_t st) {
     if constexpr (std::is_same<Elt, EltBF16>::value) return launch_small_out_t<MF, Elt, true>(a, st);
@@ -287,6 +323,15 @@ hipError_t launch_small_front(const FwdArgs& a, hipStream_t st) { return by_rows
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t st) { return by_rows<SmallCore>(a, st); }
 hipError_t launch_small_out(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOut>(a, st); }
 hipError_t launch_small_out_kr(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOutKR>(a, st); }
+hipError_t launch_small_front_raw(const FwdArgs& a, hipStream_t st) { return by_rows<SmallFrontRaw>(a, st); }
+hipError_t launch_small_core_epi(const FwdArgs& a, hipStream_t st) { return by_rows<SmallCoreEpi>(a, st); }
+hipError_t launch_small_out_epi(const FwdArgs& a, hipStream_t st) { return by_rows<SmallOutEpi>(a, st); }
+
+bool small_epi_fused_ok(const FwdArgs& a) {
+  const int mf = small_mf(a.T);
+  const size_t stat = (size_t)mf * 256 * (1 + kSkW) * sizeof(float);   // SkLds<MF, kSkW>
+  return stat + dev::sk_epi_dyn_bytes(mf, a) <= (size_t)160 * 1024 && a.r3 % 8 == 0;
+}
 
 hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t st) {
   if (a0.dtype != kDtypeBF16 || a0.r3 != 256 || a0.E_pad != a1.E_pad || a0.r3 != a1.r3) {
