@@ -124,4 +124,6 @@ def sha256(t: torch.Tensor) -> str:
     t = t.detach().contiguous().cpu()
     if t.dtype == torch.bfloat16:
         t = t.view(torch.int16)
+    elif t.dtype == torch.float8_e4m3fn:
+        t = t.view(torch.uint8)
     return hashlib.sha256(t.numpy().tobytes()).hexdigest()
