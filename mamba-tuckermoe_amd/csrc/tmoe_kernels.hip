@@ -5,6 +5,7 @@
 #include "tmoe_small.hpp"
 #include "tmoe_latent.hpp"
 #include "tmoe_outproj_wide.hpp"
+#include "tmoe_outproj_mid.hpp"
 
 namespace tmoe {
 namespace {
@@ -177,6 +178,16 @@ int cu_count() {
 // 256 rows (the workspace rounds its tile rows to 256 for these plans), and at
 // least one tile per compute unit (fewer leave units idle, where k_outproj_pp's
 // smaller tiles do better).
+// k_outproj_mid's contract: as k_outproj_wide's with 144-column tiles and A rows
+// rounded to 128 (within the 256 of the workspace), and at most one tile per
+// compute unit: a second round measured slower than k_outproj_pp's bigger tiles
+// (C3 shapes, T = 4096: 38 us against 33 us)
+bool outproj_mid_ok(const FwdArgs& a, int64_t ncu) {
+  if (a.dtype != kDtypeBF16 || a.out_scale || a.epi_mode != kEpiNone) return false;
+  if (a.r2 % 64 != 0 || a.d_out % dev::mid::BN != 0 || !a.mid_rows_256) return false;
+  return cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN) <= ncu;
+}
+
 bool outproj_wide_ok(const FwdArgs& a, int64_t ncu) {
   if (a.dtype != kDtypeBF16 || a.out_scale || a.epi_mode != kEpiNone) return false;
   if (a.r2 % 64 != 0 || a.d_out % dev::wide::BN != 0 || !a.mid_rows_256) return false;
@@ -192,6 +203,13 @@ hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
     const int64_t wt = cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN);
     const dim3 grid((unsigned)(wt < ncu ? wt : ncu)), block(256);
     hipLaunchKernelGGL(dev::k_outproj_wide, grid, block, 0, st,
+                       static_cast<const uint16_t*>(a.mid), static_cast<const uint16_t*>(a.uoutT),
+                       static_cast<uint16_t*>(a.out), a.bias, (int)a.T, (int)a.d_out, (int)a.r2);
+    return hipGetLastError();
+  }
+  if (outproj_mid_ok(a, ncu)) {
+    const dim3 grid((unsigned)(cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN))), block(256);
+    hipLaunchKernelGGL(dev::k_outproj_mid, grid, block, 0, st,
                        static_cast<const uint16_t*>(a.mid), static_cast<const uint16_t*>(a.uoutT),
                        static_cast<uint16_t*>(a.out), a.bias, (int)a.T, (int)a.d_out, (int)a.r2);
     return hipGetLastError();

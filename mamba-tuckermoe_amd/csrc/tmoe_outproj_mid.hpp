@@ -1,0 +1,148 @@
+// The mid-T bf16 out-projection out = A W^T + bias (reference: model.py:101's
+// `core @ self.U_out + bias`; A = mid or, folded, c (x) z): 128 x 144 output
+// tiles, so that T = 2048 at d_out = 2304 gives 16 x 16 = 256 work-groups, one per
+// compute unit (the 256 x 192 and 128 x 192 tiles of k_outproj_pp gave 96-192,
+// each walking its K loop with one tile in flight).
+//
+// 4 waves, one per SIMD; a wave owns 32 tokens x 144 columns as 2 x 9 blocks of
+// 16 x 16 (v_mfma_f32_16x16x32_bf16, W^T fragment first: lane l holds token
+// l & 15 of its row block and columns 4 (l >> 4) .. + 3 of its column block).
+// K tiles of 64 stream by DMA into four LDS stages of 272 rows (128 of A, 144 of
+// W^T), three tiles ahead of the MFMAs: in this regime every work-group has one
+// tile and the time is the DMA latency each K tile would otherwise expose.
+// The bias is loaded at the start (each lane's 4 columns of each block).
+//
+// Shape contract (checked by the host): K % 64 == 0, N % 144 == 0, A allocated
+// for T rounded up to 128 rows (rows past T are read, their results never
+// stored), no column scale, no fused epilogue.
+#pragma once
+
+namespace tmoe {
+namespace dev {
+
+namespace mid {
+
+constexpr int BM = 128;          // tokens per tile
+constexpr int BN = 144;          // columns per tile
+constexpr int FM = 2;            // 16-row blocks per wave (32 tokens)
+constexpr int FN = 9;            // 16-column blocks per wave (all 144)
+constexpr int NS = 4;            // LDS stages
+constexpr int kRows = BM + BN;   // 272 operand rows per K tile
+constexpr int kStage = kRows * 8;          // 16-byte slots per stage
+constexpr int kBlocks = kRows / 8;         // 34 DMA blocks of 8 rows
+constexpr int kABlocks = BM / 8;           // 16
+constexpr int kDmaPerWave = (kBlocks + 3) / 4;   // 9 (the last block repeats)
+static_assert(NS * kStage * 16 <= 160 * 1024, "LDS");
+static_assert((NS - 1) * kDmaPerWave <= 63, "vmcnt range");
+
+}  // namespace mid
+
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2m __attribute__((ext_vector_type(2)));
+
+// A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32.
+__global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict__ A,
+                                                     const uint16_t* __restrict__ Bt,
+                                                     uint16_t* __restrict__ C,
+                                                     const float* __restrict__ bias, int M,
+                                                     int N, int K) {
+  using namespace mid;
+  __shared__ u32x4 smem[NS * kStage];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ntn = N / BN;
+  const int ntiles = ((M + BM - 1) / BM) * ntn;
+  const int nkt = K / 64;
+  const int64_t row_bytes = (int64_t)K * 2;
+  int tm, tn;
+  tile_coords_of(blockIdx.x, ntn, ntiles, tm, tn);
+  const int n0 = tn * BN;
+
+  // this lane's bias columns: block j, columns 16 j + 4 (lane >> 4) + 0..3
+  float4 bv[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+    bv[j] = *reinterpret_cast<const float4*>(bias + n0 + j * 16 + 4 * (lane >> 4));
+
+  // DMA instruction d of this wave: block min(wave + 4 d, kBlocks - 1); blocks
+  // below kABlocks are A rows, the rest W^T rows
+  const char* abase = reinterpret_cast<const char*>(A) + (int64_t)tm * BM * row_bytes;
+  const char* bbase = reinterpret_cast<const char*>(Bt) + (int64_t)n0 * row_bytes;
+  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
+    u32x4* s = smem + stage * kStage;
+#pragma unroll
+    for (int d = 0; d < kDmaPerWave; ++d) {
+      const int blk = cmin_dev(wave + 4 * d, kBlocks - 1);
+      const int r = 8 * blk + (lane >> 3);   // stage row
+      const char* src = blk < kABlocks ? abase + (int64_t)r * row_bytes
+                                       : bbase + (int64_t)(r - BM) * row_bytes;
+      src += (int64_t)kt * kTileKBytes + dma_chunk(lane, blk) * 16;
+      // the LDS address goes through an integer (as in k_outproj_wide): with a
+      // pointer the compiler makes the fragment reads of the other stages wait for
+      // this DMA
+      const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) u32x4*)(s + blk * 64);
+      __builtin_amdgcn_global_load_lds((gbl_cvptr)src, (lds_vptr)(size_t)lds, 16, 0, 0);
+    }
+  };
+
+  f32x4m acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4m{0.f, 0.f, 0.f, 0.f};
+
+  // prologue: tiles 0 .. NS - 2 in flight (those that exist)
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < nkt) dma(t, t);
+
+  static_assert(NS == 4, "the waits below count two tiles after tile kt");
+  for (int kt = 0; kt < nkt; ++kt) {
+    // tile kt has landed once at most the DMAs of the tiles issued after it
+    // (kt + 1, kt + 2, as far as they exist) remain
+    if (kt + 2 < nkt) wait_vm_lds<2 * kDmaPerWave>();
+    else if (kt + 1 < nkt) wait_vm_lds<kDmaPerWave>();
+    else wait_vm_lds<0>();
+    lds_barrier();
+    // tile kt + NS - 1 into the stage tile kt - 1 used (every read of it ended
+    // before the barrier above)
+    if (kt + NS - 1 < nkt) dma(kt + NS - 1, (kt + NS - 1) % NS);
+    const u32x4* s = smem + (kt % NS) * kStage;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = ks * 4 + (lane >> 4);
+      u32x4 af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = s[lds_slot(wave * 32 + i * 16 + (lane & 15), ch)];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = s[lds_slot(BM + j * 16 + (lane & 15), ch)];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, bf[j]), __builtin_bit_cast(bf16x8, af[i]), acc[i][j], 0,
+              0, 0);
+    }
+  }
+  mfma_drain();
+
+  // epilogue: lane l holds token 32 wave + 16 i + (l & 15), columns 16 j + 4 (l >> 4)
+  // + 0..3: one 8-byte store per block
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int row = tm * BM + wave * 32 + i * 16 + (lane & 15);
+    if (row < M) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        u32x2m v;
+        v.x = pack_bf16x2(acc[i][j][0] + bv[j].x, acc[i][j][1] + bv[j].y);
+        v.y = pack_bf16x2(acc[i][j][2] + bv[j].z, acc[i][j][3] + bv[j].w);
+        *reinterpret_cast<u32x2m*>(C + (int64_t)row * N + n0 + j * 16 + 4 * (lane >> 4)) = v;
+      }
+    }
+  }
+}
+
+}  // namespace dev
+}  // namespace tmoe

@@ -101,6 +101,27 @@ def test_wide_outproj_ragged(pkg, dev, T, fold):
     _check(w, got, onp.forward_f64(x, params, w.k), f"C3/T={T}/fold={fold}")
 
 
+# The 128 x 144-tile out-projection (k_outproj_mid) between the small-T kernels and
+# k_outproj_wide: ragged last row tiles, a K of 256 and two column tiles.
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+@pytest.mark.parametrize("T", [257, 777, 2000, 2048])
+def test_mid_outproj_ragged(pkg, dev, T, fold):
+    w = pkg.WORKLOADS["C3"]
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, T, stream=6)
+    got = _run(_module(pkg, dev, w, params, fold), x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"C3/T={T}/fold={fold}")
+
+
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+def test_mid_outproj_narrow(pkg, dev, fold):
+    w = pkg.Workload("custom", 1500, 256, 288, 8, 2, 2, 128, 256, torch.bfloat16, 79)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    got = _run(_module(pkg, dev, w, params, fold), x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"mid narrow/fold={fold}")
+
+
 @pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
 def test_wide_outproj_narrow(pkg, dev, fold):
     # (E, k, r1, r3, r2, d_in, d_out): K = 256 either way, 2 column tiles of 288
