@@ -173,25 +173,13 @@ int cu_count() {
   return n;
 }
 
-// k_outproj_wide's contract: bf16, no column scale, no fused epilogue, K a
-// multiple of 64, whole 288-column tiles, A (mid) allocated for T rounded up to
-// 256 rows (the workspace rounds its tile rows to 256 for these plans), and at
-// least one tile per compute unit (fewer leave units idle, where k_outproj_pp's
-// smaller tiles do better).
-// k_outproj_mid's contract: as k_outproj_wide's with 144-column tiles and A rows
-// rounded to 128 (within the 256 of the workspace), and at most one tile per
-// compute unit: a second round measured slower than k_outproj_pp's bigger tiles
-// (C3 shapes, T = 4096: 38 us against 33 us)
-bool outproj_mid_ok(const FwdArgs& a, int64_t ncu) {
+// k_outproj_wide / k_outproj_mid's contract: bf16, no column scale, no fused
+// epilogue, K a multiple of 64, whole 288- (144-) column tiles, A (mid) allocated
+// for T rounded up to 256 rows (the workspace rounds its tile rows to 256 for
+// these plans).
+bool outproj_tiled_ok(const FwdArgs& a) {
   if (a.dtype != kDtypeBF16 || a.out_scale || a.epi_mode != kEpiNone) return false;
-  if (a.r2 % 64 != 0 || a.d_out % dev::mid::BN != 0 || !a.mid_rows_256) return false;
-  return cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN) <= ncu;
-}
-
-bool outproj_wide_ok(const FwdArgs& a, int64_t ncu) {
-  if (a.dtype != kDtypeBF16 || a.out_scale || a.epi_mode != kEpiNone) return false;
-  if (a.r2 % 64 != 0 || a.d_out % dev::wide::BN != 0 || !a.mid_rows_256) return false;
-  return cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN) >= ncu;
+  return a.r2 % 64 == 0 && a.d_out % dev::wide::BN == 0 && a.mid_rows_256;
 }
 
 // bf16 out-projection: persistent, one work-group per compute unit (its LDS
@@ -199,19 +187,31 @@ bool outproj_wide_ok(const FwdArgs& a, int64_t ncu) {
 hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
   typedef OutCfgBF16 C;
   const int64_t ncu = cu_count();
-  if (outproj_wide_ok(a, ncu)) {
-    const int64_t wt = cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN);
-    const dim3 grid((unsigned)(wt < ncu ? wt : ncu)), block(256);
-    hipLaunchKernelGGL(dev::k_outproj_wide, grid, block, 0, st,
-                       static_cast<const uint16_t*>(a.mid), static_cast<const uint16_t*>(a.uoutT),
-                       static_cast<uint16_t*>(a.out), a.bias, (int)a.T, (int)a.d_out, (int)a.r2);
-    return hipGetLastError();
-  }
-  if (outproj_mid_ok(a, ncu)) {
-    const dim3 grid((unsigned)(cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN))), block(256);
-    hipLaunchKernelGGL(dev::k_outproj_mid, grid, block, 0, st,
-                       static_cast<const uint16_t*>(a.mid), static_cast<const uint16_t*>(a.uoutT),
-                       static_cast<uint16_t*>(a.out), a.bias, (int)a.T, (int)a.d_out, (int)a.r2);
+  if (outproj_tiled_ok(a)) {
+    // measured at d_out = 2304, K = 1024 (plain GEMM, us): T = 2048: 128 x 144 tiles
+    // 19.3, 128 x 288 23.8, 256 x 288 32.8; T = 4096: 36.2, 26.4, 34.0; T = 6144:
+    // 52.2, 42.7, 35.8; T = 8192: 69.4, 47.8, 39.5 (k_outproj_pp: 27 at 2048, 31 at
+    // 4096). The smallest tile whose count fits one round of compute units wins
+    // up to T = 4096; above, the 256 x 288 tiles, also in a partial round.
+    const uint16_t* A = static_cast<const uint16_t*>(a.mid);
+    const uint16_t* Bt = static_cast<const uint16_t*>(a.uoutT);
+    uint16_t* out = static_cast<uint16_t*>(a.out);
+    const int T = (int)a.T, N = (int)a.d_out, K = (int)a.r2;
+    const int64_t ntn = a.d_out / dev::wide::BN;
+    const int64_t t_mid = cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN);
+    const int64_t t128 = cdiv(a.T, dev::wide::Cfg<1>::BM) * ntn;
+    const int64_t t256 = cdiv(a.T, dev::wide::Cfg<2>::BM) * ntn;
+    if (t_mid <= ncu) {
+      hipLaunchKernelGGL(dev::k_outproj_mid, dim3((unsigned)t_mid), dim3(256), 0, st, A, Bt, out,
+                         a.bias, T, N, K);
+    } else if (t128 <= ncu) {
+      hipLaunchKernelGGL(dev::k_outproj_wide<1>, dim3((unsigned)t128), dim3(256), 0, st, A, Bt,
+                         out, a.bias, T, N, K);
+    } else {
+      const dim3 grid((unsigned)(t256 < ncu ? t256 : ncu));
+      hipLaunchKernelGGL(dev::k_outproj_wide<2>, grid, dim3(256), 0, st, A, Bt, out, a.bias, T, N,
+                         K);
+    }
     return hipGetLastError();
   }
   const int64_t tiles = (int64_t)cdiv(a.T, C::BM) * cdiv(a.d_out, C::BN);

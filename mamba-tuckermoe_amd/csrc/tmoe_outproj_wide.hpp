@@ -3,12 +3,13 @@
 // here with A = mid or, for folded plans, c (x) z, and W^T = U_out^T or
 // (core U_out)^T).
 //
-// One work-group of 4 waves per compute unit, one wave per SIMD. A wave owns 64
-// rows x 288 columns: 18 accumulator blocks of 32 x 32, 16 of them pinned to the
-// AGPRs and 2 to VGPRs through inline-asm MFMAs (builtin MFMAs on this many
+// One work-group of 4 waves per compute unit, one wave per SIMD. A wave owns 32 FM
+// rows x 288 columns (tiles of 128 FM tokens, FM = 2 for large T, 1 for mid-size
+// T): 9 FM accumulator blocks of 32 x 32, up to 16 of them pinned to the AGPRs and
+// the rest to VGPRs through inline-asm MFMAs (builtin MFMAs on this many
 // accumulators made the compiler copy them between the register files around
 // every MFMA). K tiles of 64 (128 bytes of a row) stream by DMA into two LDS
-// stages of 544 rows (256 of A, 288 of W^T) with the swizzle of lds_slot.
+// stages of BM + 288 rows (A, then W^T) with the swizzle of lds_slot.
 //
 // The epilogue stores come from the accumulators directly (lanes l and l + 32
 // swap halves with v_permlane32_swap so that each lane writes 16 contiguous
@@ -30,19 +31,27 @@ namespace dev {
 
 namespace wide {
 
-constexpr int BM = 256;          // tokens per tile
 constexpr int FN = 9;            // 32-column blocks per tile
 constexpr int BN = 32 * FN;      // 288 columns
-constexpr int FM = 2;            // 32-row blocks per wave (64 rows)
 constexpr int kAgprBlk = 16;     // accumulator blocks in AGPRs; the rest in VGPRs
-constexpr int kRows = BM + BN;   // operand rows per K tile
-constexpr int kStage = kRows * 8;       // 16-byte slots per stage
-constexpr int kBlocks = kRows / 8;      // 8-row DMA blocks per stage
-constexpr int kDmaPerWave = kBlocks / 4;
-constexpr int kABlocksPerWave = BM / 32;
-constexpr int kStores = 2 * FN * FM;    // epilogue stores per wave of a full tile
-static_assert(kBlocks % 4 == 0, "DMA blocks split evenly over 4 waves");
-static_assert(kDmaPerWave + kStores <= 63, "counted waits within the vmcnt range");
+
+// Tiles of BM = 128 FM tokens: FM 32-row blocks per wave (FM = 2: 256 x 288, the
+// large-T tile; FM = 1: 128 x 288, twice as many tiles for mid-size T).
+template <int FM_>
+struct Cfg {
+  static constexpr int FM = FM_;
+  static constexpr int BM = 128 * FM;
+  static constexpr int kRows = BM + BN;            // operand rows per K tile
+  static constexpr int kStage = kRows * 8;         // 16-byte slots per stage
+  static constexpr int kBlocks = kRows / 8;        // 8-row DMA blocks per stage
+  static constexpr int kDmaPerWave = kBlocks / 4;
+  static constexpr int kABlocksPerWave = BM / 32;
+  static constexpr int kStores = 2 * FN * FM;      // epilogue stores per wave of a full tile
+  static_assert(kBlocks % 4 == 0, "DMA blocks split evenly over 4 waves");
+  static_assert(kDmaPerWave + kStores <= 63, "counted waits within the vmcnt range");
+  static_assert(2 * kStage * 16 <= 160 * 1024, "LDS");
+};
+constexpr int BM = Cfg<2>::BM;   // the large-T tile
 
 }  // namespace wide
 
@@ -59,15 +68,14 @@ static_assert(kDmaPerWave + kStores <= 63, "counted waits within the vmcnt range
 // result: lane l holds row l & 31 of the block and columns 8 q + 4 (l >> 5) +
 // 0..3 in elements 4 q .. 4 q + 3). ld(b) runs after the b-th MFMA: the next
 // step's fragment reads, spread between the MFMAs.
-template <bool kZero, class LD>
-__device__ __forceinline__ void wide_step(f32x16 (&acc)[wide::FM][wide::FN],
-                                          const u32x4 (&af)[wide::FM],
+template <bool kZero, int FM, class LD>
+__device__ __forceinline__ void wide_step(f32x16 (&acc)[FM][wide::FN], const u32x4 (&af)[FM],
                                           const u32x4 (&bf)[wide::FN], LD&& ld) {
 #pragma unroll
   for (int j = 0; j < wide::FN; ++j)
 #pragma unroll
-    for (int i = 0; i < wide::FM; ++i) {
-      const int blk = j * wide::FM + i;
+    for (int i = 0; i < FM; ++i) {
+      const int blk = j * FM + i;
       if (kZero) {
         if (blk < wide::kAgprBlk) TMOE_MFMA_A0(acc[i][j], bf[j], af[i]);
         else TMOE_MFMA_V0(acc[i][j], bf[j], af[i]);
@@ -78,17 +86,27 @@ __device__ __forceinline__ void wide_step(f32x16 (&acc)[wide::FM][wide::FN],
       ld(blk);
       __builtin_amdgcn_sched_barrier(0);
     }
+  // fewer MFMAs than fragments (FM = 1: 9 against 10): the rest after the last
+#pragma unroll
+  for (int m = FM * wide::FN; m < FM + wide::FN; ++m) ld(m);
 }
 
 // A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32. The pointers
 // are separate restrict parameters: that lets the compiler read bias through
 // the scalar unit (it may assume no store of C clobbers it).
+template <int FM_>
 __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict__ A,
                                                       const uint16_t* __restrict__ Bt,
                                                       uint16_t* __restrict__ C,
                                                       const float* __restrict__ bias, int M,
                                                       int N, int K) {
-  using namespace wide;
+  using wide::FN;
+  using wide::BN;
+  using wide::kAgprBlk;
+  typedef wide::Cfg<FM_> Cf;
+  constexpr int FM = Cf::FM, BM = Cf::BM, kStage = Cf::kStage;
+  constexpr int kDmaPerWave = Cf::kDmaPerWave, kABlocksPerWave = Cf::kABlocksPerWave;
+  constexpr int kStores = Cf::kStores;
   __shared__ u32x4 smem[2 * kStage];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -128,7 +146,7 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
   auto read_frag = [&](int kt, int ks, int buf, int m) __attribute__((always_inline)) {
     const u32x4* s = smem + (kt & 1) * kStage;
     const int ch = ks * 2 + (lane >> 5);
-    if (m < FM) fa[buf][m] = s[lds_slot(wave * 64 + m * 32 + (lane & 31), ch)];
+    if (m < FM) fa[buf][m] = s[lds_slot(wave * (32 * FM) + m * 32 + (lane & 31), ch)];
     else if (m < FM + FN) fb[buf][m - FM] = s[lds_slot(BM + (m - FM) * 32 + (lane & 31), ch)];
   };
   auto read_frags = [&](int kt, int ks, int buf) __attribute__((always_inline)) {
@@ -150,8 +168,8 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
     __builtin_amdgcn_sched_barrier(0);
     {
       auto ld = [&](int m) __attribute__((always_inline)) { read_frag(kt, 1, 1, m); };
-      if (first) wide_step<true>(acc, fa[0], fb[0], ld);
-      else wide_step<false>(acc, fa[0], fb[0], ld);
+      if (first) wide_step<true, FM>(acc, fa[0], fb[0], ld);
+      else wide_step<false, FM>(acc, fa[0], fb[0], ld);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (more && issue) {
@@ -159,16 +177,16 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
       for (int d = kDmaPerWave / 2; d < kDmaPerWave; ++d) dma(d, kt + 1, (kt + 1) & 1, tm, tn);
     }
     __builtin_amdgcn_sched_barrier(0);
-    wide_step<false>(acc, fa[1], fb[1],
+    wide_step<false, FM>(acc, fa[1], fb[1],
                      [&](int m) __attribute__((always_inline)) { read_frag(kt, 2, 0, m); });
     __builtin_amdgcn_sched_barrier(0);
-    wide_step<false>(acc, fa[0], fb[0],
+    wide_step<false, FM>(acc, fa[0], fb[0],
                      [&](int m) __attribute__((always_inline)) { read_frag(kt, 3, 1, m); });
     __builtin_amdgcn_sched_barrier(0);
     if (keep_stores) wait_vm_lds<kStores>();
     else wait_vm_lds<0>();
     lds_barrier();
-    wide_step<false>(acc, fa[1], fb[1], [&](int m) __attribute__((always_inline)) {
+    wide_step<false, FM>(acc, fa[1], fb[1], [&](int m) __attribute__((always_inline)) {
       if (more) read_frag(kt + 1, 0, 0, m);
     });
     __builtin_amdgcn_sched_barrier(0);
@@ -212,7 +230,7 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
       int ln = threadIdx.x & 63;
       asm volatile("" : "+v"(ln));
       const int n0 = tn * BN;
-      const int m0 = tm * BM + wave * 64;
+      const int m0 = tm * BM + wave * (32 * FM);
       const bool hi = ln >= 32;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {

@@ -101,10 +101,11 @@ def test_wide_outproj_ragged(pkg, dev, T, fold):
     _check(w, got, onp.forward_f64(x, params, w.k), f"C3/T={T}/fold={fold}")
 
 
-# The 128 x 144-tile out-projection (k_outproj_mid) between the small-T kernels and
-# k_outproj_wide: ragged last row tiles, a K of 256 and two column tiles.
+# Mid-size T: the 128 x 144-tile out-projection (k_outproj_mid, T <= 2048 at the C3
+# shapes) and the 128 x 288 tiles of k_outproj_wide<1> (2048 < T <= 4096): ragged
+# last row tiles, a K of 256 and two column tiles.
 @pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
-@pytest.mark.parametrize("T", [257, 777, 2000, 2048])
+@pytest.mark.parametrize("T", [257, 777, 2000, 2048, 3001, 4096])
 def test_mid_outproj_ragged(pkg, dev, T, fold):
     w = pkg.WORKLOADS["C3"]
     params = pkg.synth.make_params(w, affine="random")
