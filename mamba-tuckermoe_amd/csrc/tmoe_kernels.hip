@@ -347,6 +347,9 @@ hipError_t launch_small_out_epi(const FwdArgs& a, hipStream_t st) { return by_ro
 
 bool small_epi_fused_ok(const FwdArgs& a) {
   const int mf = small_mf(a.T);
+  // a wave runs the epilogue of MF 16 / 16 tokens one after the other: at 4 (T > 32)
+  // the separate epilogue kernel measured faster (C1, T = 64: 36.0 us against 32.6)
+  if (mf > 2) return false;
   const size_t stat = (size_t)mf * 256 * (1 + kSkW) * sizeof(float);   // SkLds<MF, kSkW>
   return stat + dev::sk_epi_dyn_bytes(mf, a) <= (size_t)160 * 1024 && a.r3 % 8 == 0;
 }
