@@ -84,7 +84,7 @@ hipEvent_t prof_event() {
 }
 
 struct Layout {
-  size_t z, c, idx, w, mid, raw, mpart, total;
+  size_t z, c, idx, w, mid, raw, mpart, sync, total;
   int split, fsplit;
 };
 
@@ -116,6 +116,9 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
     L.mpart = o;
     o = align256(o + (size_t)L.split * tile_rows * p->s.r2 * sizeof(float));
   }
+  // error word and flags of the kernels that signal between work-groups
+  L.sync = o;
+  if (T > 0) o = align256(o + (size_t)tmoe::sync_words(T) * sizeof(uint32_t));
   L.total = o;
   return L;
 }
@@ -160,6 +163,7 @@ tmoe::FwdArgs make_args(const tmoe_plan* p, const void* x, int64_t T, const void
   a.mpart = L.mpart ? reinterpret_cast<float*>(ws + L.mpart) : nullptr;
   a.core_split = L.split;
   a.front_split = L.fsplit;
+  a.sync = reinterpret_cast<uint32_t*>(ws + L.sync);
   return a;
 }
 

@@ -69,7 +69,27 @@ struct FwdArgs {
   int epi_mode;
   const void* epi_a;            // (T, d_out) dtype     gate output / residual input
   const void* epi_b;            // (d_out) dtype        LayerScale gamma
+  // signals between the work-groups of one launch (kernels that publish data for
+  // other work-groups of the same grid): sync[0] records a wait that ran out of
+  // time, sync[sync_flag(i)] is flag i; epoch is the value a flag takes when
+  // published, drawn fresh by the launcher (next_epoch)
+  uint32_t* sync;
+  uint32_t epoch;
 };
+
+// FwdArgs::sync: the error word, then one flag per 32-token tile of the largest T a
+// launch that signals may have, each flag alone in its 256-byte block (polls and
+// publications of different flags do not meet on one cache line)
+constexpr int64_t kSyncTileRows = 32;
+constexpr int64_t kSyncStride = 64;   // words
+constexpr int64_t sync_words(int64_t T) {
+  return kSyncStride * (1 + (T + kSyncTileRows - 1) / kSyncTileRows);
+}
+constexpr int64_t sync_flag(int64_t i) { return kSyncStride * (1 + i); }
+// a nonzero value no earlier launch of this process used (the counter starts at a
+// random point, so words a previous process left in reused memory match with
+// probability 2^-32)
+uint32_t next_epoch();
 
 // fused out-projection epilogues (TMOE_EPI_* of include/tmoe.h)
 constexpr int kEpiNone = 0, kEpiGlu = 1, kEpiResScale = 2;

@@ -1,5 +1,6 @@
 // Launch configurations of the gfx950 kernels (device code: tmoe_kernels.hpp).
 #include <atomic>
+#include <chrono>
 
 #include "tmoe_kernels.hpp"
 #include "tmoe_small.hpp"
@@ -56,9 +57,13 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
     }
   }
   if constexpr (R3 == 256 && NR == 8 && std::is_same<Elt, EltBF16>::value) {
-    // z and router work-groups of 32 tokens (k_front_split), three LDS stages
+    // router and z work-groups of 32 tokens (k_front_split), three LDS stages;
+    // with c (x) z to write, the z work-groups wait for the router's c (a fresh
+    // epoch for the signals)
+    FwdArgs b = a;
+    b.epoch = next_epoch();
     const dim3 grid(2 * cdiv(a.T, 32)), block(256);
-    hipLaunchKernelGGL((dev::k_front_split<Elt, R3, NR, kFrontPFA, 3>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((dev::k_front_split<Elt, R3, NR, kFrontPFA, 3>), grid, block, 0, st, b);
     return hipGetLastError();
   }
   constexpr int BM = NR >= 8 ? 32 : kFrontBM, WM = NR >= 8 ? 1 : kFrontWM;
@@ -427,7 +432,24 @@ bool front_fuses_cz(const FwdArgs& a) {
   // c fits over the logits for r1 <= 32, BM x (E_pad + 1) floats)
   if (a.dtype != kDtypeBF16 || a.T <= kSmallT) return false;
   if (a.front_split > 1) return true;
-  return a.r1 <= 32 && !(a.r3 == 256 && a.E_pad == 256);
+  // k_front_split (r3 = 256, E_pad = 256): the z work-groups wait for the router
+  // work-groups' c through the workspace's sync words
+  if (a.r3 == 256 && a.E_pad == 256) return a.r1 <= 32 && a.sync != nullptr;
+  return a.r1 <= 32;
+}
+
+uint32_t next_epoch() {
+  // a random start (clock and an address of this image), then one per launch
+  static std::atomic<uint32_t> ctr{[] {
+    uint64_t v = (uint64_t)std::chrono::high_resolution_clock::now().time_since_epoch().count();
+    v ^= (uint64_t)(uintptr_t)&ctr * 0x9e3779b97f4a7c15ull;
+    return (uint32_t)(v ^ (v >> 32));
+  }()};
+  uint32_t e;
+  do {
+    e = ctr.fetch_add(1, std::memory_order_relaxed) + 1;
+  } while (e == 0);
+  return e;
 }
 
 hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t st) {

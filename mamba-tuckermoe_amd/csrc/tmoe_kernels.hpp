@@ -838,6 +838,62 @@ __device__ __forceinline__ void flush_tile_by(const char* stage, const FwdArgs& 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 
+// ---- signals between the work-groups of one launch -------------------------
+// A producer work-group writes the data it hands over with device-scope stores
+// (store_coherent), then sets a flag word to the launch's epoch; its consumer
+// waits for that value and reads the data with device-scope loads
+// (load_coherent). Both sides go through the point of coherence of the XCDs'
+// caches for those words only: release and acquire fences would write back or
+// invalidate the whole L2 of an XCD, under the work-groups still computing there
+// (measured: the E_pad = 256 front at T = 4096 went from 35 to 72 us with an
+// acquire in the wait loop). sync_publish waits for the work-group's stores to
+// complete before the flag is written.
+// Consumers have higher work-group indices than their producers (work-groups
+// start in index order, so a waiting consumer never keeps its producer from
+// starting), wait at most kSyncLimitTicks of the 100 MHz real-time clock (past
+// it, sync[0] records the epoch and the consumer goes on with NaN in place of the
+// data), and set the flag back to 0 once they have seen it, so that a graph
+// replay of the same launch (same epoch) waits again.
+constexpr uint64_t kSyncLimitTicks = 2000000;   // 20 ms
+
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void sync_publish(uint32_t* flag, uint32_t epoch) {
+  wait_vm_lds<0>();   // this thread's stores have completed (the barrier alone
+  __syncthreads();    // does not wait for them), then every thread's have
+  if (threadIdx.x == 0)
+    __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread; true once the flag was seen, false when the wait ran out
+// of time. seen_all: one word of the kernel's LDS array for the answer (a
+// __shared__ variable of its own changed how the compiler tracks the kernel's LDS
+// DMA: it then waited for every DMA before each fragment read of the main loop).
+__device__ __forceinline__ bool sync_await(uint32_t* flag, uint32_t epoch, uint32_t* err,
+                                           int* seen_all) {
+  if (threadIdx.x == 0) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    int seen = 1;
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncLimitTicks) {
+        seen = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);   // ~512 clocks between polls
+    }
+    if (seen) __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *seen_all = seen;
+  }
+  __syncthreads();
+  return *seen_all != 0;
+}
+
 // ---- k_front: in-projection + RMSNorm, router + top-k + softmax + c --------
 // model.py:75-81 (+ the U_expert gather of :93 folded into c). One work-group:
 // BM tokens x (R3 z columns + EP router columns), NW = R3 / 32 (at most 4) waves
@@ -1384,11 +1440,15 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
 }
 
 // The front for wide routers (E_pad = 32 NR > 128 with r3 = R3 = 256), in two kinds
-// of work-group over 32-token tiles: the first ceil(T / 32) compute z (x against
-// U_in^T, RMSNorm), the others the logits (x against the router rows, top-k,
-// softmax, c). The two halves are independent, and splitting them doubles the
-// work-groups (128 of the single kind at T = 4096 left half of 256 CUs idle) and
-// halves the weight rows each streams. 4 waves each, wave tile 32 x (columns / 4).
+// of work-group over 32-token tiles: the first ceil(T / 32) compute the logits (x
+// against the router rows, top-k, softmax, c), the others z (x against U_in^T,
+// RMSNorm). Splitting them doubles the work-groups (128 of the single kind at T =
+// 4096 left half of 256 CUs idle) and halves the weight rows each streams. 4 waves
+// each, wave tile 32 x (columns / 4). Folded plans (a.cz set): router work-group tm
+// hands its tile's c to z work-group tm through sync flag tm (device-scope stores
+// and loads, sync_publish / sync_await), which then writes the tile's c (x) z rows
+// from its staged z in place of z (the separate k_expand_cz pass it replaces took
+// 6-8 us at T = 4096).
 template <class Elt, int R3, int NR, int PFA, int NS>
 __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
   typedef typename Elt::T T;
@@ -1400,13 +1460,16 @@ __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
   constexpr int kZEpi = TileStage<TLZ, T>::kBytes + (NW * BM + BM) * 4;
   constexpr int kREpi = (BM * LD + kTopkRecFloats<BM>) * 4;
   constexpr int kUe = 4096;   // U_expert (E = 256, r1 = 4) when it fits
+  constexpr int kCRows = BM * 32 * 4 + 16;   // c rows of the tile (r1 <= 32), a flag word
   constexpr int kSmemBytes =
-      cmax(cmax(TLZ::kLdsBytes, TLR::kLdsBytes), cmax(kZEpi, kREpi + kUe));
+      cmax(cmax(TLZ::kLdsBytes, TLR::kLdsBytes), cmax(kZEpi + kCRows, kREpi + kUe));
   __shared__ u32x4 smem[kSmemBytes / 16];
 
   const int ntm = (int)((a.T + BM - 1) / BM);
-  const bool zpart = (int)blockIdx.x < ntm;   // uniform over the work-group
-  const int tm = zpart ? (int)blockIdx.x : (int)blockIdx.x - ntm;
+  // router work-groups first: with a.cz set, z work-group tm waits for router
+  // work-group tm's c (sync flag tm) and writes the tile's c (x) z rows itself
+  const bool zpart = (int)blockIdx.x >= ntm;   // uniform over the work-group
+  const int tm = zpart ? (int)blockIdx.x - ntm : (int)blockIdx.x;
   const int64_t m0 = (int64_t)tm * BM;
   const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
   const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
@@ -1420,6 +1483,20 @@ __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
     char* zst = reinterpret_cast<char*>(smem);
     front_z_epilogue<TLZ, Elt, R3>(acc, a, m0, rows_valid, zst,
                                    reinterpret_cast<float*>(zst + TileStage<TLZ, T>::kBytes));
+    if constexpr (std::is_same<Elt, EltBF16>::value) {
+      if (a.cz) {
+        // c of the tile's rows from the router work-group, into LDS after the
+        // RMSNorm partials; NaN when the wait ran out of time
+        float* cl = reinterpret_cast<float*>(zst + kZEpi);
+        const bool ok = sync_await(a.sync + sync_flag(tm), a.epoch, a.sync,
+                                   reinterpret_cast<int*>(cl + BM * 32));
+        const int n = rows_valid * (int)a.r1;
+        for (int q = threadIdx.x; q < n; q += TLZ::kThreads)
+          cl[q] = ok ? load_coherent(a.c + m0 * a.r1 + q) : __builtin_nanf("");
+        __syncthreads();
+        flush_cz<TLZ, R3>(zst, cl, a, m0, rows_valid);
+      }
+    }
   } else {
     RowLoader bl{reinterpret_cast<const char*>(a.wfront) + R3 * row_bytes, row_bytes, EP};
     f32x16 acc[TLR::FM][TLR::FN];
@@ -1435,8 +1512,15 @@ __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
           lg[(i * 32 + acc_row(lane, e)) * LD + wn * TLR::kWaveN + j * 32 + (lane & 31)] =
               acc[i][j][e];
     __syncthreads();
+    // c also into LDS over the logits (read before the top-k record is complete)
     front_topk<EP, BM, TLR::kThreads, 1>(a, m0, rows_valid, lg, LD, lg + BM * LD,
-                                         kSmemBytes - kREpi);
+                                         kSmemBytes - kREpi, a.cz ? lg : nullptr);
+    if (a.cz) {   // c of the tile's rows for z work-group tm, device-scope
+      __syncthreads();
+      const int n = rows_valid * (int)a.r1;
+      for (int q = threadIdx.x; q < n; q += TLR::kThreads) store_coherent(a.c + m0 * a.r1 + q, lg[q]);
+      sync_publish(a.sync + sync_flag(tm), a.epoch);
+    }
   }
 }
 

@@ -268,6 +268,50 @@ def test_side_stream(pkg, dev):
     assert torch.equal(out, ref)
 
 
+def test_signal_workspace_reuse_and_graph_replay(pkg, dev):
+    """The E_pad = 256 front signals between its work-groups (the z work-groups wait
+    for the router work-groups' c through flag words in the workspace). The result
+    does not depend on what the workspace held before (0xFF bytes, random bytes, the
+    flags a previous forward left), and replays of a captured graph (the same epoch
+    each time) equal the eager forward."""
+    w = pkg.WORKLOADS["C4"]
+    T = 600
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, T, stream=7).to(dev)
+    m = _module(pkg, dev, w, params, True)
+    plan, packed = m.plan(), m.packed()
+    L = pkg._lib.lib()
+    with torch.no_grad():
+        ref = m(x)
+    ws_bytes = plan.workspace_bytes(T)
+    g = torch.Generator(device=dev).manual_seed(3)
+    fills = [torch.full((ws_bytes,), 255, dtype=torch.uint8, device=dev),
+             torch.randint(0, 256, (ws_bytes,), dtype=torch.uint8, device=dev, generator=g)]
+    for ws in fills:
+        for _ in range(2):   # the second call finds the first one's flags
+            out = torch.empty_like(ref)
+            pkg._lib.check(L.tmoe_forward(plan.ptr, x.data_ptr(), T, packed.data_ptr(),
+                                          out.data_ptr(), None, None, None, ws.data_ptr(),
+                                          ws_bytes, torch.cuda.current_stream().cuda_stream))
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out_g = torch.empty_like(ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph, stream=s):
+        m.forward_raw(x, out=out_g)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref)
+        with torch.no_grad():
+            assert torch.equal(m(x), ref)   # eager work between the replays
+        torch.cuda.synchronize()
+
+
 def _fp8_reference(params, codes):
     """float64 state_dict of the fp8 layer: bf16 router / U_expert / gain / bias
     and the oracle's dequantisation of the e4m3 weights."""
