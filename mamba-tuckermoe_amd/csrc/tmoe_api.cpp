@@ -106,8 +106,13 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   L.mid = o; o = align256(o + (size_t)tile_rows * mid_cols * p->es);
   L.raw = o;
   L.fsplit = tmoe::front_split(T, p->s.d_in, p->E_pad, p->kdtype == TMOE_BF16);
-  if (T <= tmoe::kSmallT || L.fsplit > 1)
-    o = align256(o + (size_t)L.fsplit * T * (p->s.r3 + p->s.E) * sizeof(float));
+  if (T <= tmoe::kSmallT || L.fsplit > 1) {
+    int64_t raw_floats = L.fsplit * T * (p->s.r3 + p->s.E);
+    // the one-launch decode's scratch (z columns, sums of squares, c)
+    if (T <= tmoe::kDecodeMaxT)
+      raw_floats = std::max(raw_floats, tmoe::sk_decode_scratch_floats(T, p->s.r3, p->rk));
+    o = align256(o + (size_t)raw_floats * sizeof(float));
+  }
   // k_core_pp in rank groups: fp32 partial sums of mid
   L.mpart = 0;
   L.split = 1;
@@ -118,7 +123,9 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   }
   // error word and flags of the kernels that signal between work-groups
   L.sync = o;
-  if (T > 0) o = align256(o + (size_t)tmoe::sync_words(T) * sizeof(uint32_t));
+  if (T > 0)
+    o = align256(o + (size_t)tmoe::sync_words(T, T <= tmoe::kDecodeMaxT ? p->s.r3 / 16 + 1 : 0) *
+                         sizeof(uint32_t));
   L.total = o;
   return L;
 }
@@ -198,8 +205,12 @@ using Launch = hipError_t (*)(const tmoe::FwdArgs&, hipStream_t);
 // The small-T stages (front, core, out-projection) of a forward with args a: the
 // front epilogue runs inside the core (or, folded, the out-projection) when that
 // kernel's LDS holds it, else as its own kernel after the front's GEMM.
-void small_stages(const tmoe::FwdArgs& a, bool fold, Launch (&st)[kStages]) {
-  if (tmoe::small_epi_fused_ok(a)) {
+void small_stages(const tmoe::FwdArgs& a, bool fold, hipStream_t stream, Launch (&st)[kStages]) {
+  if (fold && tmoe::small_decode_ok(a, stream)) {   // one launch
+    st[0] = tmoe::launch_small_decode;
+    st[1] = launch_nothing;
+    st[2] = launch_nothing;
+  } else if (tmoe::small_epi_fused_ok(a)) {
     st[0] = tmoe::launch_small_front_raw;
     st[1] = fold ? launch_nothing : tmoe::launch_small_core_epi;
     st[2] = fold ? tmoe::launch_small_out_epi : tmoe::launch_small_out;
@@ -511,7 +522,7 @@ int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packe
                                     tmoe::launch_outproj};
   // folded: the out-projection builds c (x) z from z and c itself (no core stage)
   Launch small_path[kStages];
-  small_stages(a, fold, small_path);
+  small_stages(a, fold, st, small_path);
   const Launch* stages = small ? small_path : big_path;
   const char* stage_names[kStages] = {"front (router + in-projection)", "core",
                                       "out-projection"};
@@ -623,7 +634,7 @@ int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* p
   if (T <= tmoe::kSmallT) {
     for (const tmoe::FwdArgs* a : {&g, &u}) {
       Launch small[kStages];
-      small_stages(*a, p->fold, small);
+      small_stages(*a, p->fold, st, small);
       for (int i = 0; i < kStages; ++i)
         if ((e = small[i](*a, st)) != hipSuccess) return hip_fail(e, "tmoe_forward_glu");
     }

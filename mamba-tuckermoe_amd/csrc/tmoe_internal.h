@@ -82,8 +82,11 @@ struct FwdArgs {
 // publications of different flags do not meet on one cache line)
 constexpr int64_t kSyncTileRows = 32;
 constexpr int64_t kSyncStride = 64;   // words
-constexpr int64_t sync_words(int64_t T) {
-  return kSyncStride * (1 + (T + kSyncTileRows - 1) / kSyncTileRows);
+// flags: one per 32-token tile, at least min_flags (the small-T decode kernel's
+// producers)
+constexpr int64_t sync_words(int64_t T, int64_t min_flags = 0) {
+  return kSyncStride * (1 + ((T + kSyncTileRows - 1) / kSyncTileRows > min_flags
+                                 ? (T + kSyncTileRows - 1) / kSyncTileRows : min_flags));
 }
 constexpr int64_t sync_flag(int64_t i) { return kSyncStride * (1 + i); }
 // a nonzero value no earlier launch of this process used (the counter starts at a
@@ -190,6 +193,16 @@ hipError_t launch_small_front_raw(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_core_epi(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_out_epi(const FwdArgs& a, hipStream_t stream);
 bool small_epi_fused_ok(const FwdArgs& a);
+// the whole small-T folded layer in one launch (k_sk_decode): bf16, T <= 64,
+// T r3 <= 16384, E <= 16, r1 <= 32, r3 % 16 == 0, sync words present, and the
+// stream not being captured
+bool small_decode_ok(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_small_decode(const FwdArgs& a, hipStream_t stream);
+constexpr int64_t kDecodeMaxT = 64;
+// floats of its scratch at FwdArgs::raw: z columns (T, r3), c (T, r1)
+constexpr int64_t sk_decode_scratch_floats(int64_t T, int64_t r3, int64_t r1) {
+  return T * r3 + T * r1;
+}
 // folded plans (T > kSmallT): mid (T, r1*r3) = c (x) z, the Khatri-Rao row product
 // mid[t, r*r3 + s] = c[t, r] z[t, s] rounded to bf16; launch_outproj then runs with
 // r2 := r1 * r3 and uoutT := W^T

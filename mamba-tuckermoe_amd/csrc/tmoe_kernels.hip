@@ -359,6 +359,38 @@ bool small_epi_fused_ok(const FwdArgs& a) {
   return stat + dev::sk_epi_dyn_bytes(mf, a) <= (size_t)160 * 1024 && a.r3 % 8 == 0;
 }
 
+bool small_decode_ok(const FwdArgs& a, hipStream_t st) {
+  if (a.dtype != kDtypeBF16 || a.T > kDecodeMaxT || a.T * a.r3 > 16384 || a.E > 16 ||
+      a.r3 % 16 != 0 || !a.sync || a.r1 > 32)
+    return false;
+  const int mf = small_mf(a.T);
+  const size_t stat = (size_t)mf * 256 * (1 + kSkW) * sizeof(float);   // SkLds<MF, kSkW>
+  if (stat + dev::sk_decode_dyn_bytes(mf, a) > (size_t)160 * 1024) return false;
+  // the consumers wait on flags that stay set (several per flag): a replayed graph
+  // would find them set, so a captured forward takes the two-launch path
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  return true;
+}
+
+template <int MF>
+hipError_t launch_small_decode_t(const FwdArgs& a, hipStream_t st) {
+  FwdArgs b = a;
+  b.epoch = next_epoch();
+  const dim3 grid((unsigned)(a.r3 / 16 + 1 + cdiv(a.d_out, 16))), block(64 * kSkW);
+  hipLaunchKernelGGL((dev::k_sk_decode<MF, kSkW>), grid, block, dev::sk_decode_dyn_bytes(MF, a),
+                     st, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_small_decode(const FwdArgs& a, hipStream_t st) {
+  switch (small_mf(a.T)) {
+    case 1: return launch_small_decode_t<1>(a, st);
+    case 2: return launch_small_decode_t<2>(a, st);
+    default: return launch_small_decode_t<4>(a, st);
+  }
+}
+
 hipError_t launch_front_pair(const FwdArgs& a0, const FwdArgs& a1, hipStream_t st) {
   if (a0.dtype != kDtypeBF16 || a0.r3 != 256 || a0.E_pad != a1.E_pad || a0.r3 != a1.r3) {
     if (hipError_t e = launch_front(a0, st); e != hipSuccess) return e;

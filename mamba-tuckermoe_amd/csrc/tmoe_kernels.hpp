@@ -852,8 +852,8 @@ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 // start in index order, so a waiting consumer never keeps its producer from
 // starting), wait at most kSyncLimitTicks of the 100 MHz real-time clock (past
 // it, sync[0] records the epoch and the consumer goes on with NaN in place of the
-// data), and set the flag back to 0 once they have seen it, so that a graph
-// replay of the same launch (same epoch) waits again.
+// data), and, when a flag has one consumer, that consumer sets it back to 0 once
+// seen, so that a graph replay of the same launch (same epoch) waits again.
 constexpr uint64_t kSyncLimitTicks = 2000000;   // 20 ms
 
 __device__ __forceinline__ void store_coherent(float* p, float v) {
@@ -870,25 +870,41 @@ __device__ __forceinline__ void sync_publish(uint32_t* flag, uint32_t epoch) {
     __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Called by every thread; true once the flag was seen, false when the wait ran out
-// of time. seen_all: one word of the kernel's LDS array for the answer (a
-// __shared__ variable of its own changed how the compiler tracks the kernel's LDS
-// DMA: it then waited for every DMA before each fragment read of the main loop).
-__device__ __forceinline__ bool sync_await(uint32_t* flag, uint32_t epoch, uint32_t* err,
-                                           int* seen_all) {
-  if (threadIdx.x == 0) {
+// Called by every thread: waits for the n flags flags[0], flags[kSyncStride], ...;
+// true once all were seen, false when the wait ran out of time. The first wave
+// polls: lane l watches flags l, l + 64, ..., so that flags set at about the same
+// time cost one round trip, not one each. reset: the caller is the flags' only
+// consumer and sets them back to 0 (a flag several work-groups wait for stays
+// set; such launches are not replayed from a graph). seen_all: one word of the
+// kernel's LDS array for the answer (a __shared__ variable of its own changed how
+// the compiler tracks the kernel's LDS DMA: it then waited for every DMA before
+// each fragment read of the main loop). The work-group has at least 64 threads.
+__device__ __forceinline__ bool sync_await(uint32_t* flags, int n, uint32_t epoch, uint32_t* err,
+                                           int* seen_all, bool reset) {
+  if (threadIdx.x < 64) {   // the whole first wave
+    const int l = threadIdx.x;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    int seen = 1;
-    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+    int next = l;   // the lane's first flag not yet seen
+    bool seen = true;
+    while (true) {
+      while (next < n && __hip_atomic_load(flags + (int64_t)next * kSyncStride, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == epoch)
+        next += 64;
+      if (__all(next >= n)) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncLimitTicks) {
-        seen = 0;
+        seen = false;
         break;
       }
       __builtin_amdgcn_s_sleep(8);   // ~512 clocks between polls
     }
-    if (seen) __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *seen_all = seen;
+    if (!seen) {
+      if (l == 0) __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (reset) {
+      for (int i = l; i < n; i += 64)
+        __hip_atomic_store(flags + (int64_t)i * kSyncStride, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (l == 0) *seen_all = seen ? 1 : 0;
   }
   __syncthreads();
   return *seen_all != 0;
@@ -1488,8 +1504,8 @@ __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
         // c of the tile's rows from the router work-group, into LDS after the
         // RMSNorm partials; NaN when the wait ran out of time
         float* cl = reinterpret_cast<float*>(zst + kZEpi);
-        const bool ok = sync_await(a.sync + sync_flag(tm), a.epoch, a.sync,
-                                   reinterpret_cast<int*>(cl + BM * 32));
+        const bool ok = sync_await(a.sync + sync_flag(tm), 1, a.epoch, a.sync,
+                                   reinterpret_cast<int*>(cl + BM * 32), true);
         const int n = rows_valid * (int)a.r1;
         for (int q = threadIdx.x; q < n; q += TLZ::kThreads)
           cl[q] = ok ? load_coherent(a.c + m0 * a.r1 + q) : __builtin_nanf("");

@@ -505,6 +505,252 @@ __global__ __launch_bounds__(64 * W) void k_sk_epi_gemm(FwdArgs a) {
   }
 }
 
+// ---- the small-T folded layer in one launch (decode) -----------------------
+// Producers: work-groups 0 .. NZ - 1 (NZ = r3 / 16) compute 16 columns of z each
+// (x U_in, skinny_tile; fp8 plans: the column scales) and publish them;
+// work-group NZ computes the router logits (E <= 16 columns), runs the routing
+// epilogue of every token (route_row16: one 16-lane row per token, four tokens a
+// wave) and publishes c. Consumers: the other work-groups own 16 columns of out
+// each; they load their GEMM's first weight chunks, wait for the NZ + 1 producers
+// (sync flags 0 .. NZ, several consumers per flag, so no flag is reset: the
+// launcher does not use this kernel under graph capture), load z and c, form
+// z = RMSNorm(z) * gain and its bf16 rounding into LDS, and run the GEMM of
+// k_sk_epi_gemm against W^T with A = c (x) z from LDS. Producer data crosses the
+// work-groups through the scratch at a.raw, 16 bytes per device-scope access:
+// zr (T, r3) fp32, cs (T, r1) fp32. T <= MF * 16: one token block; the z a thread
+// loads is held in registers (kDecodeGroups 4-column groups per thread).
+struct SkDecodeScratch {
+  float *zr, *cs;
+  __device__ __forceinline__ SkDecodeScratch(const FwdArgs& a) {
+    zr = a.raw;
+    cs = zr + a.T * a.r3;
+  }
+};
+constexpr int kDecodeGroups = 4;
+// Dynamic LDS bytes of k_sk_decode: the router's U_expert and c rows; a
+// consumer's z rows (bf16), c rows and 1 / rms.
+inline size_t sk_decode_dyn_bytes(int mf, const FwdArgs& a) {
+  const size_t rows = (size_t)mf * 16;
+  const size_t router = ((size_t)a.E * a.r1 + rows * a.r1) * 4;
+  const size_t consumer = rows * a.r3 * 2 + rows * a.r1 * 4 + rows * 4;
+  return router > consumer ? router : consumer;
+}
+
+// 16-byte device-scope accesses: buffer instructions with the sc1 cache policy
+// (the path of store_coherent / load_coherent, four words at a time). n_floats
+// bounds the descriptor: an offset past it reads 0 and writes nothing.
+constexpr int kCPolSC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* base,
+                                                                int64_t n_floats) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0,
+                                           (int)(n_floats * 4), 0x00020000);
+}
+__device__ __forceinline__ f32x4 load_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCPolSC1));
+}
+__device__ __forceinline__ void store_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, kCPolSC1);
+}
+
+// The routing epilogue of token t on one 16-lane row of a wave (sl: the lane's
+// index in the row; E <= 16, K <= E, r1 <= 32; every lane of the row calls it):
+// epi_finish's routing with the row's DPP steps in place of the wave's (the same
+// selection rounds, slot order and sums), c into c_row (LDS) and a's outputs.
+__device__ __forceinline__ void route_row16(const FwdArgs& a, int64_t t, int sl, float lv,
+                                            const float* ue, float* c_row) {
+  const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
+  const int mode = a.router_mode;
+  if (a.logits && sl < E) a.logits[t * E + sl] = lv;
+  const float sv = mode ? capped_score(lv, a.router_scale, a.router_temperature) : lv;
+  uint64_t key = sl < E ? rank_key(sv, sl) : 0;
+  float selv = 0.f, vmax = 0.f;
+  int si = 0;
+#pragma unroll 1
+  for (int kk = 0; kk < K; ++kk) {
+    uint64_t best = key;
+    group_max_key<8>(best);
+    dpp_max_step<0x140>(best);   // row_mirror: the two 8-lane halves
+    key = key == best ? 0 : key;
+    if (kk == 0) vmax = key_value(best);
+    if (kk == sl) {
+      selv = key_value(best);
+      si = key_index(best);
+    }
+  }
+  const float ex = sl < K ? expf(selv - vmax) : 0.f;
+  float ssum = ex;
+  group_sum<8>(ssum);
+  dpp_add_step<0x140>(ssum);
+  float wk;
+  if (mode) {
+    float sa = sl < E ? expf(sv - vmax) : 0.f;
+    group_sum<8>(sa);
+    dpp_add_step<0x140>(sa);
+    float ps = 0.f;
+    for (int j = 0; j < K; ++j) ps += __shfl(ex, j, 16) / sa;
+    wk = (ex / sa) / (ps + 1e-6f);
+  } else {
+    wk = ex / ssum;
+  }
+  if (sl < K) {
+    a.idx[t * K + sl] = si;
+    a.w[t * K + sl] = wk;
+  }
+  float c0 = 0.f, c1 = 0.f;
+#pragma unroll 1
+  for (int kk = 0; kk < K; ++kk) {
+    const float w = __shfl(wk, kk, 16);
+    const int i = __shfl(si, kk, 16);
+    if (sl < R1) c0 += w * ue[i * R1 + sl];
+    if (sl + 16 < R1) c1 += w * ue[i * R1 + sl + 16];
+  }
+  if (sl < R1) {
+    a.c[t * R1 + sl] = c0;
+    c_row[sl] = c0;
+  }
+  if (sl + 16 < R1) {
+    a.c[t * R1 + sl + 16] = c1;
+    c_row[sl + 16] = c1;
+  }
+}
+
+template <int MF, int W>
+__global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
+  static_assert(W == 16, "one 16-lane row per token of a 64-token block");
+  typedef EltBF16 Elt;
+  typedef typename Elt::T T;
+  __shared__ float red[SkLds<MF, W>::kFloats];
+  extern __shared__ u32x4 dynv[];
+  float* dyn = reinterpret_cast<float*>(dynv);
+  const int R3 = (int)a.r3, R1 = (int)a.r1, E = (int)a.E, NZ = R3 / 16;
+  const int Tn = (int)a.T;
+  const int bid = blockIdx.x;
+  const SkDecodeScratch sc(a);
+  if (bid <= NZ) {
+    // ---- producers: 16 columns of [z | logits] for every token ----
+    const int64_t rbx = a.d_in * (int64_t)sizeof(T);
+    const int64_t n0 = (int64_t)bid * 16;
+    const int cols_valid = bid < NZ ? 16 : E;
+    // the router's U_expert, loaded under the GEMM (E r1 <= 512 floats)
+    const float uev = bid == NZ && threadIdx.x < E * R1 ? a.uexp[threadIdx.x] : 0.f;
+    SkRows<Elt> as{reinterpret_cast<const char*>(a.x), rbx, Tn};
+    skinny_tile<Elt, MF, W, 2>(as, reinterpret_cast<const char*>(a.wfront) + n0 * rbx, rbx,
+                               cols_valid, a.d_in, red);
+    if (bid < NZ) {
+      // z columns (scaled: fp8 plans), four to a store
+      const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
+      for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
+        const int row = e >> 2, g = e & 3;
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          v[j] = a.zscale ? red[row * 16 + g * 4 + j] * a.zscale[n0 + g * 4 + j]
+                          : red[row * 16 + g * 4 + j];
+        store_coherent4(rz, (int)(((int64_t)row * R3 + n0 + g * 4) * 4), v);
+      }
+    } else {
+      // the routing epilogue of every token; c into LDS, then published
+      float* ue = dyn;             // (E, r1)
+      float* cl = ue + E * R1;     // (MF 16, r1)
+      if (threadIdx.x < E * R1) ue[threadIdx.x] = uev;
+      __syncthreads();
+      const int sl = threadIdx.x & 15;
+      for (int t = threadIdx.x >> 4; t < Tn; t += 4 * W)   // row-uniform
+        route_row16(a, t, sl, sl < E ? red[t * 16 + sl] : 0.f, ue, cl + t * R1);
+      __syncthreads();
+      for (int q = threadIdx.x; q < Tn * R1; q += 64 * W) store_coherent(sc.cs + q, cl[q]);
+    }
+    sync_publish(a.sync + sync_flag(bid), a.epoch);
+    return;
+  }
+  // ---- consumers: 16 columns of out = (c (x) z) W^T + bias ----
+  T* zl = reinterpret_cast<T*>(dyn);                          // (MF 16, r3)
+  float* cl = reinterpret_cast<float*>(zl + MF * 16 * R3);    // (MF 16, r1)
+  float* inv = cl + MF * 16 * R1;                             // (MF 16)
+  float* part = red + 64;                                     // (T, r3 / 4) partial sums
+  const int64_t n0 = (int64_t)(bid - NZ - 1) * 16;
+  const int64_t K = (int64_t)R1 * R3;
+  const int64_t rb = K * (int64_t)sizeof(T);
+  const int cols_valid = (int)(a.d_out - n0 < 16 ? a.d_out - n0 : 16);
+  const char* bsrc = reinterpret_cast<const char*>(a.uoutT) + n0 * rb;
+  // under the wait: the GEMM's first weight chunks, and the gain of the z groups
+  // g = thread + 64 W j (4 columns each) this thread normalises
+  u32x4 bpre[1][2];
+  skinny_b_first<Elt, W, 1>(bsrc, rb, cols_valid, K, bpre);
+  const int G = R3 / 4, NG = Tn * G;
+  float gv[kDecodeGroups][4];
+#pragma unroll
+  for (int j = 0; j < kDecodeGroups; ++j) {
+    const int g = threadIdx.x + 64 * W * j;
+    const int col = (g - (g / G) * G) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) gv[j][q] = g < NG ? a.gain[col + q] : 0.f;
+  }
+  const bool ok = sync_await(a.sync + sync_flag(0), NZ + 1, a.epoch, a.sync,
+                             reinterpret_cast<int*>(red), false);
+  // every load first: the z groups, c
+  const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
+  f32x4 zv[kDecodeGroups];
+#pragma unroll
+  for (int j = 0; j < kDecodeGroups; ++j) {
+    const int g = threadIdx.x + 64 * W * j;
+    zv[j] = load_coherent4(rz, g < NG ? g * 16 : Tn * R3 * 4);   // past the end: 0
+  }
+#pragma unroll
+  for (int j = 0; j < kDecodeGroups; ++j) {
+    const int g = threadIdx.x + 64 * W * j;
+    if (g < NG)
+      part[g] = ((zv[j][0] * zv[j][0] + zv[j][1] * zv[j][1]) + zv[j][2] * zv[j][2]) +
+                zv[j][3] * zv[j][3];
+  }
+  for (int q = threadIdx.x; q < Tn * R1; q += 64 * W)
+    cl[q] = ok ? load_coherent(sc.cs + q) : __builtin_nanf("");
+  __syncthreads();
+  {
+    // each row's sum of squares: 16 lanes over its groups, then the row's DPP sum
+    const int row = threadIdx.x >> 4, sl = threadIdx.x & 15;
+    if (row < Tn) {   // row-uniform
+      float s = 0.f;
+      for (int g = sl; g < G; g += 16) s += part[row * G + g];
+      group_sum<8>(s);
+      dpp_add_step<0x140>(s);
+      if (sl == 0) inv[row] = 1.f / sqrtf(s / (float)R3 + a.eps);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kDecodeGroups; ++j) {
+    const int g = threadIdx.x + 64 * W * j;
+    if (g < NG) {
+      const int row = g / G;
+      const float ir = inv[row];
+      // z as stored by epi_finish: R((z / rms) * gain)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) store_from_f32(zl + g * 4 + q, (zv[j][q] * ir) * gv[j][q]);
+    }
+  }
+  __syncthreads();
+  SkKhatriRaoLds<Elt> as{zl, cl, R1, R3, Tn};
+  const int c = threadIdx.x & 15;
+  const float bias = c < cols_valid ? a.bias[n0 + c] : 0.f;
+  const float osc = a.out_scale && c < cols_valid ? a.out_scale[n0 + c] : 1.f;
+  skinny_tile<Elt, MF, W, 1, SkKhatriRaoLds<Elt>, true>(as, bsrc, rb, cols_valid, K, red, 0,
+                                                        nullptr, 0, bpre);
+  for (int e = threadIdx.x; e < MF * 256; e += 64 * W) {
+    const int row = e >> 4;
+    if (row < Tn && c < cols_valid) {
+      const int64_t oi = (int64_t)row * a.d_out + n0 + c;
+      float y = red[e] * osc + bias;
+      if (a.epi_mode != kEpiNone)
+        y = epi_value<Elt>(a.epi_mode, round_as(y, Elt{}),
+                           load_as_f32(static_cast<const T*>(a.epi_a) + oi),
+                           a.epi_mode == kEpiResScale
+                               ? load_as_f32(static_cast<const T*>(a.epi_b) + n0 + c) : 0.f);
+      store_from_f32(reinterpret_cast<T*>(a.out) + oi, y);
+    }
+  }
+}
+
 // mid (T, r2) = (c (x) z) core^T; fp8 weights: rank r's partial sums scaled by
 // core_scale_raw[r, q]
 template <class Elt, int MF, int W>

@@ -312,6 +312,60 @@ def test_signal_workspace_reuse_and_graph_replay(pkg, dev):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("T", [1, 17, 32, 64])
+def test_decode_one_launch_workspace_and_graph(pkg, dev, T):
+    """Decode-sized folded forwards run as one launch whose out-projection
+    work-groups wait for the front's work-groups (flags in the workspace). Against
+    the float64 oracle on workspaces pre-filled with 0xFF and random bytes (twice
+    each, the second call finding the first one's flags, all bit-equal); under graph
+    capture the library takes the two-launch path, whose replays match the oracle
+    and route identically."""
+    w = pkg.WORKLOADS["C2"]
+    params = pkg.synth.make_params(w, affine="random")
+    x_cpu = pkg.synth.make_x(w, T, stream=11)
+    x = x_cpu.to(dev)
+    m = _module(pkg, dev, w, params, True)
+    plan, packed = m.plan(), m.packed()
+    assert plan.folded()
+    L = pkg._lib.lib()
+    ref64 = onp.forward_f64(x_cpu, params, w.k)
+    ws_bytes = plan.workspace_bytes(T)
+    g = torch.Generator(device=dev).manual_seed(5)
+    fills = [torch.full((ws_bytes,), 255, dtype=torch.uint8, device=dev),
+             torch.randint(0, 256, (ws_bytes,), dtype=torch.uint8, device=dev, generator=g)]
+    first = None
+    for ws in fills:
+        for _ in range(2):
+            out = torch.empty(T, w.d_out, dtype=w.dtype, device=dev)
+            idx = torch.empty(T, w.k, dtype=torch.int32, device=dev)
+            pkg._lib.check(L.tmoe_forward(plan.ptr, x.data_ptr(), T, packed.data_ptr(),
+                                          out.data_ptr(), idx.data_ptr(), None, None,
+                                          ws.data_ptr(), ws_bytes,
+                                          torch.cuda.current_stream().cuda_stream))
+            torch.cuda.synchronize()
+            if first is None:
+                first = out.clone()
+                assert (idx.cpu().numpy() == ref64["idx"]).all()
+                assert onp.rel_l2(out.float().cpu().numpy(), ref64["out"]) <= TOL[w.dtype]
+            assert torch.equal(out, first)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out_g = torch.empty(T, w.d_out, dtype=w.dtype, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph, stream=s):
+        _, idx_g, _, _ = m.forward_raw(x, routing=True, out=out_g)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert (idx_g.cpu().numpy() == ref64["idx"]).all()
+        assert onp.rel_l2(out_g.float().cpu().numpy(), ref64["out"]) <= TOL[w.dtype]
+        with torch.no_grad():
+            assert torch.equal(m(x), first)   # eager (one launch) between the replays
+        torch.cuda.synchronize()
+
+
 def _fp8_reference(params, codes):
     """float64 state_dict of the fp8 layer: bf16 router / U_expert / gain / bias
     and the oracle's dequantisation of the e4m3 weights."""
