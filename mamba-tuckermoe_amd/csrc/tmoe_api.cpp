@@ -124,7 +124,8 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   // error word and flags of the kernels that signal between work-groups
   L.sync = o;
   if (T > 0)
-    o = align256(o + (size_t)tmoe::sync_words(T, T <= tmoe::kDecodeMaxT ? p->s.r3 / 16 + 1 : 0) *
+    o = align256(o + (size_t)tmoe::sync_words(
+                             T, T <= tmoe::kDecodeMaxT ? tmoe::sk_decode_flags(p->s.r3) : 0) *
                          sizeof(uint32_t));
   L.total = o;
   return L;

@@ -194,15 +194,19 @@ hipError_t launch_small_core_epi(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_out_epi(const FwdArgs& a, hipStream_t stream);
 bool small_epi_fused_ok(const FwdArgs& a);
 // the whole small-T folded layer in one launch (k_sk_decode): bf16, T <= 64,
-// T r3 <= 16384, E <= 16, r1 <= 32, r3 % 16 == 0, sync words present, and the
-// stream not being captured
+// T r3 <= 16384, E <= 16, r1 <= 32, r3 in {64, 128, 256}, sync words present, and
+// the stream not being captured
 bool small_decode_ok(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_decode(const FwdArgs& a, hipStream_t stream);
 constexpr int64_t kDecodeMaxT = 64;
-// floats of its scratch at FwdArgs::raw: z columns (T, r3), c (T, r1)
+// floats of its scratch at FwdArgs::raw: z columns (T, r3), c (T, r1), and up to
+// three partial (T, 16) tiles of each of the r3 / 16 + 1 column blocks (d_in in up
+// to four K slices)
 constexpr int64_t sk_decode_scratch_floats(int64_t T, int64_t r3, int64_t r1) {
-  return T * r3 + T * r1;
+  return T * r3 + T * r1 + (r3 / 16 + 1) * 3 * T * 16;
 }
+// its sync flags: one per producer work-group, up to four per column block
+constexpr int64_t sk_decode_flags(int64_t r3) { return (r3 / 16 + 1) * 4; }
 // folded plans (T > kSmallT): mid (T, r1*r3) = c (x) z, the Khatri-Rao row product
 // mid[t, r*r3 + s] = c[t, r] z[t, s] rounded to bf16; launch_outproj then runs with
 // r2 := r1 * r3 and uoutT := W^T

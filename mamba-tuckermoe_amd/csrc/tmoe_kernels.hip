@@ -361,7 +361,7 @@ bool small_epi_fused_ok(const FwdArgs& a) {
 
 bool small_decode_ok(const FwdArgs& a, hipStream_t st) {
   if (a.dtype != kDtypeBF16 || a.T > kDecodeMaxT || a.T * a.r3 > 16384 || a.E > 16 ||
-      a.r3 % 16 != 0 || !a.sync || a.r1 > 32)
+      (a.r3 != 64 && a.r3 != 128 && a.r3 != 256) || !a.sync || a.r1 > 32)
     return false;
   const int mf = small_mf(a.T);
   const size_t stat = (size_t)mf * 256 * (1 + kSkW) * sizeof(float);   // SkLds<MF, kSkW>
@@ -377,7 +377,8 @@ template <int MF>
 hipError_t launch_small_decode_t(const FwdArgs& a, hipStream_t st) {
   FwdArgs b = a;
   b.epoch = next_epoch();
-  const dim3 grid((unsigned)(a.r3 / 16 + 1 + cdiv(a.d_out, 16))), block(64 * kSkW);
+  const dim3 grid((unsigned)((a.r3 / 16 + 1) * dev::decode_ksplit(a.d_in) + cdiv(a.d_out, 16))),
+      block(64 * kSkW);
   hipLaunchKernelGGL((dev::k_sk_decode<MF, kSkW>), grid, block, dev::sk_decode_dyn_bytes(MF, a),
                      st, b);
   return hipGetLastError();

@@ -895,7 +895,7 @@ __device__ __forceinline__ bool sync_await(uint32_t* flags, int n, uint32_t epoc
         seen = false;
         break;
       }
-      __builtin_amdgcn_s_sleep(8);   // ~512 clocks between polls
+      __builtin_amdgcn_s_sleep(2);   // ~128 clocks between polls
     }
     if (!seen) {
       if (l == 0) __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

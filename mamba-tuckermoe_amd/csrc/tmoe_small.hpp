@@ -66,7 +66,8 @@ struct SkKhatriRao {
   __device__ __forceinline__ u32x4 chunk(int row, int64_t k) const {
     typedef typename Elt::T T;
     const int t = row < rows_valid ? row : rows_valid - 1;
-    const int r = (int)(k / r3), s = (int)(k - (int64_t)r * r3);
+    // 32-bit division (k < r1 r3 < 2^31): the 64-bit one is a long inlined routine
+    const int r = (int)((uint32_t)k / (uint32_t)r3), s = (int)k - r * r3;
     const u32x4 v = *reinterpret_cast<const u32x4*>(z + ((int64_t)t * r3 + s) * (int64_t)sizeof(T));
     const float cc = c[(int64_t)t * r1 + r];
     u32x4 o;
@@ -405,7 +406,8 @@ struct SkKhatriRaoLds {
   __device__ __forceinline__ u32x4 chunk(int row, int64_t k) const {
     typedef typename Elt::T T;
     const int t = row < rows_valid ? row : rows_valid - 1;
-    const int r = (int)(k / r3), s = (int)(k - (int64_t)r * r3);
+    // 32-bit division (k < r1 r3 < 2^31): the 64-bit one is a long inlined routine
+    const int r = (int)((uint32_t)k / (uint32_t)r3), s = (int)k - r * r3;
     const u32x4 v = *reinterpret_cast<const u32x4*>(z + t * r3 + s);
     const float cc = c[t * r1 + r];
     u32x4 o;
@@ -506,33 +508,45 @@ __global__ __launch_bounds__(64 * W) void k_sk_epi_gemm(FwdArgs a) {
 }
 
 // ---- the small-T folded layer in one launch (decode) -----------------------
-// Producers: work-groups 0 .. NZ - 1 (NZ = r3 / 16) compute 16 columns of z each
-// (x U_in, skinny_tile; fp8 plans: the column scales) and publish them;
-// work-group NZ computes the router logits (E <= 16 columns), runs the routing
-// epilogue of every token (route_row16: one 16-lane row per token, four tokens a
-// wave) and publishes c. Consumers: the other work-groups own 16 columns of out
-// each; they load their GEMM's first weight chunks, wait for the NZ + 1 producers
-// (sync flags 0 .. NZ, several consumers per flag, so no flag is reset: the
-// launcher does not use this kernel under graph capture), load z and c, form
-// z = RMSNorm(z) * gain and its bf16 rounding into LDS, and run the GEMM of
-// k_sk_epi_gemm against W^T with A = c (x) z from LDS. Producer data crosses the
-// work-groups through the scratch at a.raw, 16 bytes per device-scope access:
-// zr (T, r3) fp32, cs (T, r1) fp32. T <= MF * 16: one token block; the z a thread
-// loads is held in registers (kDecodeGroups 4-column groups per thread).
+// Producers: S work-groups per 16-column block of [z | logits] (NZ = r3 / 16 z
+// blocks, then the router block of E <= 16 logit columns), each over one K slice
+// of d_in / S (skinny_tile). Slices 0 .. S - 2 publish their partial tiles; the
+// last slice of the block waits for them, adds them in slice order (its own
+// last), and publishes the block: z columns (fp8 plans: the column scales), or,
+// for the router block, the routing epilogue of every token (route_row16: one
+// 16-lane row per token, four tokens a wave) and c. Consumers: the other
+// work-groups own 16 columns of out each; they load their GEMM's first weight
+// chunks, wait for the NZ + 1 blocks (sync flags 0 .. NZ, several consumers per
+// flag, so no flag is reset: the launcher does not use this kernel under graph
+// capture), load z and c, form z = RMSNorm(z) * gain and its bf16 rounding into
+// LDS, and run the GEMM of k_sk_epi_gemm against W^T with A = c (x) z from LDS.
+// Producer data crosses the work-groups through the scratch at a.raw, 16 bytes
+// per device-scope access: zr (T, r3) fp32, cs (T, r1) fp32, then the partial
+// tiles (T, 16) fp32 of slice s < S - 1 of block b at plane b (S - 1) + s. T <= MF
+// * 16: one token block; the z a thread loads is held in registers (kDecodeGroups
+// 4-column groups per thread).
+constexpr int decode_ksplit(int64_t d_in) {
+  return d_in % 256 == 0 ? 4 : d_in % 128 == 0 ? 2 : 1;   // slices of whole 64-element groups
+}
 struct SkDecodeScratch {
-  float *zr, *cs;
+  float *zr, *cs, *ps;
   __device__ __forceinline__ SkDecodeScratch(const FwdArgs& a) {
     zr = a.raw;
     cs = zr + a.T * a.r3;
+    ps = cs + a.T * a.r1;
   }
 };
+// sync flags: 0 .. NZ the blocks, then the slices' partial tiles
+__device__ __forceinline__ int decode_slice_flag(int nz, int s_count, int blk, int sl) {
+  return nz + 1 + blk * (s_count - 1) + sl;
+}
 constexpr int kDecodeGroups = 4;
 // Dynamic LDS bytes of k_sk_decode: the router's U_expert and c rows; a
-// consumer's z rows (bf16), c rows and 1 / rms.
+// consumer's z rows (bf16) and c rows.
 inline size_t sk_decode_dyn_bytes(int mf, const FwdArgs& a) {
   const size_t rows = (size_t)mf * 16;
   const size_t router = ((size_t)a.E * a.r1 + rows * a.r1) * 4;
-  const size_t consumer = rows * a.r3 * 2 + rows * a.r1 * 4 + rows * 4;
+  const size_t consumer = rows * a.r3 * 2 + rows * a.r1 * 4;
   return router > consumer ? router : consumer;
 }
 
@@ -550,6 +564,23 @@ __device__ __forceinline__ f32x4 load_coherent4(__amdgpu_buffer_rsrc_t r, int by
 }
 __device__ __forceinline__ void store_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off, f32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, kCPolSC1);
+}
+
+// Sum over aligned groups of G in {16, 32, 64} lanes (every lane active), the
+// result in every lane of the group: the 16-lane rows' DPP butterflies, then the
+// rows' sums read into scalars (lanes 0, 16, 32, 48) and paired. VALU and scalar
+// reads only, like wave_sum.
+__device__ __forceinline__ float lane_group_sum(float v, int G) {
+  group_sum<8>(v);
+  dpp_add_step<0x140>(v);   // row_mirror: the two 8-lane halves of a row
+  if (G == 16) return v;
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  if (G == 32) return (threadIdx.x & 63) < 32 ? r0 + r1 : r2 + r3;
+  return (r0 + r1) + (r2 + r3);
 }
 
 // The routing epilogue of token t on one 16-lane row of a wave (sl: the lane's
@@ -626,17 +657,53 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
   const int Tn = (int)a.T;
   const int bid = blockIdx.x;
   const SkDecodeScratch sc(a);
-  if (bid <= NZ) {
-    // ---- producers: 16 columns of [z | logits] for every token ----
+  const int S = decode_ksplit(a.d_in), NP = (NZ + 1) * S;
+  if (bid < NP) {
+    // ---- producers: 16 columns of [z | logits], one K slice ----
+    const int blk = bid / S, sl = bid - blk * S;
+    const int64_t ks = a.d_in / S;
     const int64_t rbx = a.d_in * (int64_t)sizeof(T);
-    const int64_t n0 = (int64_t)bid * 16;
-    const int cols_valid = bid < NZ ? 16 : E;
+    const int64_t n0 = (int64_t)blk * 16;
+    const int cols_valid = blk < NZ ? 16 : E;
+    const bool last = sl == S - 1;
     // the router's U_expert, loaded under the GEMM (E r1 <= 512 floats)
-    const float uev = bid == NZ && threadIdx.x < E * R1 ? a.uexp[threadIdx.x] : 0.f;
-    SkRows<Elt> as{reinterpret_cast<const char*>(a.x), rbx, Tn};
-    skinny_tile<Elt, MF, W, 2>(as, reinterpret_cast<const char*>(a.wfront) + n0 * rbx, rbx,
-                               cols_valid, a.d_in, red);
-    if (bid < NZ) {
+    const float uev = blk == NZ && last && threadIdx.x < E * R1 ? a.uexp[threadIdx.x] : 0.f;
+    const int64_t koff = sl * ks * (int64_t)sizeof(T);
+    SkRows<Elt> as{reinterpret_cast<const char*>(a.x) + koff, rbx, Tn};
+    skinny_tile<Elt, MF, W, 2>(as, reinterpret_cast<const char*>(a.wfront) + n0 * rbx + koff, rbx,
+                               cols_valid, ks, red);
+    const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(sc.ps, (int64_t)(NZ + 1) * (S - 1) * Tn * 16);
+    if (!last) {
+      const int plane = blk * (S - 1) + sl;
+      for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = red[e * 4 + j];
+        store_coherent4(rp, (plane * Tn * 16 + e * 4) * 4, v);
+      }
+      sync_publish(a.sync + sync_flag(decode_slice_flag(NZ, S, blk, sl)), a.epoch);
+      return;
+    }
+    if (S > 1) {
+      // the other slices' tiles, added in slice order, then this one's
+      const bool ok = sync_await(a.sync + sync_flag(decode_slice_flag(NZ, S, blk, 0)), S - 1,
+                                 a.epoch, a.sync, reinterpret_cast<int*>(red + MF * 256), true);
+      for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
+        f32x4 pv[3];   // S <= 4: every load issued before the first is used
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+          pv[q] = q < S - 1 ? load_coherent4(rp, ((blk * (S - 1) + q) * Tn * 16 + e * 4) * 4)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 v = pv[0];
+#pragma unroll
+        for (int q = 1; q < 3; ++q)
+          if (q < S - 1) v += pv[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[e * 4 + j] = ok ? v[j] + red[e * 4 + j] : __builtin_nanf("");
+      }
+      __syncthreads();
+    }
+    if (blk < NZ) {
       // z columns (scaled: fp8 plans), four to a store
       const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
       for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
@@ -654,29 +721,31 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
       float* cl = ue + E * R1;     // (MF 16, r1)
       if (threadIdx.x < E * R1) ue[threadIdx.x] = uev;
       __syncthreads();
-      const int sl = threadIdx.x & 15;
+      const int ln = threadIdx.x & 15;
       for (int t = threadIdx.x >> 4; t < Tn; t += 4 * W)   // row-uniform
-        route_row16(a, t, sl, sl < E ? red[t * 16 + sl] : 0.f, ue, cl + t * R1);
+        route_row16(a, t, ln, ln < E ? red[t * 16 + ln] : 0.f, ue, cl + t * R1);
       __syncthreads();
       for (int q = threadIdx.x; q < Tn * R1; q += 64 * W) store_coherent(sc.cs + q, cl[q]);
     }
-    sync_publish(a.sync + sync_flag(bid), a.epoch);
+    sync_publish(a.sync + sync_flag(blk), a.epoch);
     return;
   }
   // ---- consumers: 16 columns of out = (c (x) z) W^T + bias ----
   T* zl = reinterpret_cast<T*>(dyn);                          // (MF 16, r3)
   float* cl = reinterpret_cast<float*>(zl + MF * 16 * R3);    // (MF 16, r1)
-  float* inv = cl + MF * 16 * R1;                             // (MF 16)
-  float* part = red + 64;                                     // (T, r3 / 4) partial sums
-  const int64_t n0 = (int64_t)(bid - NZ - 1) * 16;
+  const int64_t n0 = (int64_t)(bid - NP) * 16;
   const int64_t K = (int64_t)R1 * R3;
   const int64_t rb = K * (int64_t)sizeof(T);
   const int cols_valid = (int)(a.d_out - n0 < 16 ? a.d_out - n0 : 16);
   const char* bsrc = reinterpret_cast<const char*>(a.uoutT) + n0 * rb;
-  // under the wait: the GEMM's first weight chunks, and the gain of the z groups
-  // g = thread + 64 W j (4 columns each) this thread normalises
+  // under the wait: the GEMM's first weight chunks, the column's bias and scale,
+  // and the gain of the z groups g = thread + 64 W j (4 columns each) this thread
+  // normalises
   u32x4 bpre[1][2];
   skinny_b_first<Elt, W, 1>(bsrc, rb, cols_valid, K, bpre);
+  const int c = threadIdx.x & 15;
+  const float bias = c < cols_valid ? a.bias[n0 + c] : 0.f;
+  const float osc = a.out_scale && c < cols_valid ? a.out_scale[n0 + c] : 1.f;
   const int G = R3 / 4, NG = Tn * G;
   float gv[kDecodeGroups][4];
 #pragma unroll
@@ -688,7 +757,7 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
   }
   const bool ok = sync_await(a.sync + sync_flag(0), NZ + 1, a.epoch, a.sync,
                              reinterpret_cast<int*>(red), false);
-  // every load first: the z groups, c
+  // every load first: the z groups and c
   const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
   f32x4 zv[kDecodeGroups];
 #pragma unroll
@@ -696,34 +765,18 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
     const int g = threadIdx.x + 64 * W * j;
     zv[j] = load_coherent4(rz, g < NG ? g * 16 : Tn * R3 * 4);   // past the end: 0
   }
-#pragma unroll
-  for (int j = 0; j < kDecodeGroups; ++j) {
-    const int g = threadIdx.x + 64 * W * j;
-    if (g < NG)
-      part[g] = ((zv[j][0] * zv[j][0] + zv[j][1] * zv[j][1]) + zv[j][2] * zv[j][2]) +
-                zv[j][3] * zv[j][3];
-  }
   for (int q = threadIdx.x; q < Tn * R1; q += 64 * W)
     cl[q] = ok ? load_coherent(sc.cs + q) : __builtin_nanf("");
-  __syncthreads();
-  {
-    // each row's sum of squares: 16 lanes over its groups, then the row's DPP sum
-    const int row = threadIdx.x >> 4, sl = threadIdx.x & 15;
-    if (row < Tn) {   // row-uniform
-      float s = 0.f;
-      for (int g = sl; g < G; g += 16) s += part[row * G + g];
-      group_sum<8>(s);
-      dpp_add_step<0x140>(s);
-      if (sl == 0) inv[row] = 1.f / sqrtf(s / (float)R3 + a.eps);
-    }
-  }
-  __syncthreads();
+  // each row's sum of squares: its G groups sit in G consecutive lanes of one wave
+  // (G = r3 / 4 in {16, 32, 64}), added by the lanes' cross-lane sum
 #pragma unroll
   for (int j = 0; j < kDecodeGroups; ++j) {
     const int g = threadIdx.x + 64 * W * j;
+    if ((g & ~63) >= NG) break;   // wave-uniform: no group of this wave left
+    const float ss = lane_group_sum(((zv[j][0] * zv[j][0] + zv[j][1] * zv[j][1]) +
+                                     zv[j][2] * zv[j][2]) + zv[j][3] * zv[j][3], G);
+    const float ir = 1.f / sqrtf(ss / (float)R3 + a.eps);
     if (g < NG) {
-      const int row = g / G;
-      const float ir = inv[row];
       // z as stored by epi_finish: R((z / rms) * gain)
 #pragma unroll
       for (int q = 0; q < 4; ++q) store_from_f32(zl + g * 4 + q, (zv[j][q] * ir) * gv[j][q]);
@@ -731,9 +784,6 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
   }
   __syncthreads();
   SkKhatriRaoLds<Elt> as{zl, cl, R1, R3, Tn};
-  const int c = threadIdx.x & 15;
-  const float bias = c < cols_valid ? a.bias[n0 + c] : 0.f;
-  const float osc = a.out_scale && c < cols_valid ? a.out_scale[n0 + c] : 1.f;
   skinny_tile<Elt, MF, W, 1, SkKhatriRaoLds<Elt>, true>(as, bsrc, rb, cols_valid, K, red, 0,
                                                         nullptr, 0, bpre);
   for (int e = threadIdx.x; e < MF * 256; e += 64 * W) {
