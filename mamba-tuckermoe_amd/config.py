@@ -115,6 +115,25 @@ class Workload:
         st["out_proj"] = T * K * 2 + self.d_out * K * 2 + 4 * self.d_out + T * self.d_out * 2
         return st
 
+    def one_launch(self, T: int, rk: int, folded: bool) -> bool:
+        """Whether a forward of T tokens is the library's single decode launch
+        (k_sk_decode; the selection rule of small_decode_ok in tmoe_kernels.hip,
+        outside graph capture)."""
+        return (folded and self.dtype == torch.bfloat16 and 0 < T <= 64 and self.E <= 16
+                and self.r3 in (64, 128, 256) and rk <= 32)
+
+    def layer_bytes_folded(self, T: Optional[int] = None, rk: Optional[int] = None) -> int:
+        """Compulsory bytes of a folded forward in one launch: x, the front weights,
+        W^T, the small fp32 vectors, the routing outputs and out (no intermediate
+        crosses HBM)."""
+        T = self.T if T is None else T
+        rk = self.r1 if rk is None else rk
+        st = self.stage_bytes_folded(T, rk)
+        es = 4 if self.dtype == torch.float32 else 2
+        K = rk * self.r3
+        return (st["front"] - T * self.r3 * es - T * self.r1 * 4
+                + st["out_proj"] - T * K * 2 + T * rk * 4)
+
     def hbm_bytes(self, T: Optional[int] = None) -> int:
         """Compulsory HBM bytes per forward: x in, out, every weight once (fp8
         workloads: the three projections at one byte plus their fp32 scales)."""
