@@ -199,13 +199,11 @@ bool small_epi_fused_ok(const FwdArgs& a);
 bool small_decode_ok(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_decode(const FwdArgs& a, hipStream_t stream);
 constexpr int64_t kDecodeMaxT = 64;
-// floats of its scratch at FwdArgs::raw: z columns (T, r3), c (T, r1), and up to
-// three partial (T, 16) tiles of each of the r3 / 16 + 1 column blocks (d_in in up
-// to four K slices)
+// floats of its scratch at FwdArgs::raw: z columns (T, r3), c (T, r1)
 constexpr int64_t sk_decode_scratch_floats(int64_t T, int64_t r3, int64_t r1) {
-  return T * r3 + T * r1 + (r3 / 16 + 1) * 3 * T * 16;
+  return T * r3 + T * r1;
 }
-// its sync flags: one per producer work-group, up to four per column block
+// its sync flags: one per producer work-group, four per column block
 constexpr int64_t sk_decode_flags(int64_t r3) { return (r3 / 16 + 1) * 4; }
 // folded plans (T > kSmallT): mid (T, r1*r3) = c (x) z, the Khatri-Rao row product
 // mid[t, r*r3 + s] = c[t, r] z[t, s] rounded to bf16; launch_outproj then runs with

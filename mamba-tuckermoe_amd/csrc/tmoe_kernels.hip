@@ -377,7 +377,7 @@ template <int MF>
 hipError_t launch_small_decode_t(const FwdArgs& a, hipStream_t st) {
   FwdArgs b = a;
   b.epoch = next_epoch();
-  const dim3 grid((unsigned)((a.r3 / 16 + 1) * dev::decode_ksplit(a.d_in) + cdiv(a.d_out, 16))),
+  const dim3 grid((unsigned)((a.r3 / 16 + 1) * dev::kDecodeRowGroups + cdiv(a.d_out, 16))),
       block(64 * kSkW);
   hipLaunchKernelGGL((dev::k_sk_decode<MF, kSkW>), grid, block, dev::sk_decode_dyn_bytes(MF, a),
                      st, b);

@@ -508,44 +508,34 @@ __global__ __launch_bounds__(64 * W) void k_sk_epi_gemm(FwdArgs a) {
 }
 
 // ---- the small-T folded layer in one launch (decode) -----------------------
-// Producers: S work-groups per 16-column block of [z | logits] (NZ = r3 / 16 z
-// blocks, then the router block of E <= 16 logit columns), each over one K slice
-// of d_in / S (skinny_tile). Slices 0 .. S - 2 publish their partial tiles; the
-// last slice of the block waits for them, adds them in slice order (its own
-// last), and publishes the block: z columns (fp8 plans: the column scales), or,
-// for the router block, the routing epilogue of every token (route_row16: one
-// 16-lane row per token, four tokens a wave) and c. Consumers: the other
-// work-groups own 16 columns of out each; they load their GEMM's first weight
-// chunks, wait for the NZ + 1 blocks (sync flags 0 .. NZ, several consumers per
-// flag, so no flag is reset: the launcher does not use this kernel under graph
-// capture), load z and c, form z = RMSNorm(z) * gain and its bf16 rounding into
-// LDS, and run the GEMM of k_sk_epi_gemm against W^T with A = c (x) z from LDS.
-// Producer data crosses the work-groups through the scratch at a.raw, 16 bytes
-// per device-scope access: zr (T, r3) fp32, cs (T, r1) fp32, then the partial
-// tiles (T, 16) fp32 of slice s < S - 1 of block b at plane b (S - 1) + s. T <= MF
-// * 16: one token block; the z a thread loads is held in registers (kDecodeGroups
-// 4-column groups per thread).
-constexpr int decode_ksplit(int64_t d_in) {
-  return d_in % 256 == 0 ? 4 : d_in % 128 == 0 ? 2 : 1;   // slices of whole 64-element groups
-}
+// Producers: kDecodeRowGroups work-groups per 16-column block of [z | logits]
+// (NZ = r3 / 16 z blocks, then the router block of E <= 16 logit columns), each
+// over up to 16 of the T tokens and all of d_in (skinny_tile): the z blocks publish
+// their z columns (fp8 plans: the column scales), the router block's work-groups
+// run the routing epilogue of their tokens (route_row16: one 16-lane row per
+// token) and publish c. Consumers: the other work-groups own 16 columns of out
+// each; they load their GEMM's first weight chunks, wait for the producers' flags
+// (sync flags 0 .. (NZ + 1) kDecodeRowGroups - 1, several consumers per flag, so
+// no flag is reset: the launcher does not use this kernel under graph capture),
+// load z and c, form z = RMSNorm(z) * gain and its bf16 rounding into LDS, and run
+// the GEMM of k_sk_epi_gemm against W^T with A = c (x) z from LDS. Producer data
+// crosses the work-groups through the scratch at a.raw, 16 bytes per device-scope
+// access: zr (T, r3) fp32, cs (T, r1) fp32. T <= MF * 16: one token block; the z a
+// thread loads is held in registers (kDecodeGroups 4-column groups per thread).
+constexpr int kDecodeRowGroups = 4;   // T <= 64: at most 16 tokens a producer
 struct SkDecodeScratch {
-  float *zr, *cs, *ps;
+  float *zr, *cs;
   __device__ __forceinline__ SkDecodeScratch(const FwdArgs& a) {
     zr = a.raw;
     cs = zr + a.T * a.r3;
-    ps = cs + a.T * a.r1;
   }
 };
-// sync flags: 0 .. NZ the blocks, then the slices' partial tiles
-__device__ __forceinline__ int decode_slice_flag(int nz, int s_count, int blk, int sl) {
-  return nz + 1 + blk * (s_count - 1) + sl;
-}
 constexpr int kDecodeGroups = 4;
-// Dynamic LDS bytes of k_sk_decode: the router's U_expert and c rows; a
+// Dynamic LDS bytes of k_sk_decode: a router work-group's U_expert and c rows; a
 // consumer's z rows (bf16) and c rows.
 inline size_t sk_decode_dyn_bytes(int mf, const FwdArgs& a) {
   const size_t rows = (size_t)mf * 16;
-  const size_t router = ((size_t)a.E * a.r1 + rows * a.r1) * 4;
+  const size_t router = ((size_t)a.E * a.r1 + 16 * a.r1) * 4;
   const size_t consumer = rows * a.r3 * 2 + rows * a.r1 * 4;
   return router > consumer ? router : consumer;
 }
@@ -657,77 +647,48 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
   const int Tn = (int)a.T;
   const int bid = blockIdx.x;
   const SkDecodeScratch sc(a);
-  const int S = decode_ksplit(a.d_in), NP = (NZ + 1) * S;
+  const int NP = (NZ + 1) * kDecodeRowGroups;
   if (bid < NP) {
-    // ---- producers: 16 columns of [z | logits], one K slice ----
-    const int blk = bid / S, sl = bid - blk * S;
-    const int64_t ks = a.d_in / S;
+    // ---- producers: 16 columns of [z | logits] for up to 16 tokens ----
+    const int blk = bid / kDecodeRowGroups, rg = bid - blk * kDecodeRowGroups;
+    const int rpg = (Tn + kDecodeRowGroups - 1) / kDecodeRowGroups;
+    const int r0 = rg * rpg, rows = Tn - r0 < rpg ? Tn - r0 : rpg;   // may be <= 0
     const int64_t rbx = a.d_in * (int64_t)sizeof(T);
     const int64_t n0 = (int64_t)blk * 16;
     const int cols_valid = blk < NZ ? 16 : E;
-    const bool last = sl == S - 1;
     // the router's U_expert, loaded under the GEMM (E r1 <= 512 floats)
-    const float uev = blk == NZ && last && threadIdx.x < E * R1 ? a.uexp[threadIdx.x] : 0.f;
-    const int64_t koff = sl * ks * (int64_t)sizeof(T);
-    SkRows<Elt> as{reinterpret_cast<const char*>(a.x) + koff, rbx, Tn};
-    skinny_tile<Elt, MF, W, 2>(as, reinterpret_cast<const char*>(a.wfront) + n0 * rbx + koff, rbx,
-                               cols_valid, ks, red);
-    const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(sc.ps, (int64_t)(NZ + 1) * (S - 1) * Tn * 16);
-    if (!last) {
-      const int plane = blk * (S - 1) + sl;
-      for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
-        f32x4 v;
+    const float uev = blk == NZ && threadIdx.x < E * R1 ? a.uexp[threadIdx.x] : 0.f;
+    if (rows > 0) {   // work-group-uniform
+      SkRows<Elt> as{reinterpret_cast<const char*>(a.x) + r0 * rbx, rbx, rows};
+      skinny_tile<Elt, 1, W, 2>(as, reinterpret_cast<const char*>(a.wfront) + n0 * rbx, rbx,
+                                cols_valid, a.d_in, red);
+      if (blk < NZ) {
+        // z columns (scaled: fp8 plans), four to a store
+        const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
+        for (int e = threadIdx.x; e < rows * 4; e += 64 * W) {
+          const int row = e >> 2, g = e & 3;
+          f32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = red[e * 4 + j];
-        store_coherent4(rp, (plane * Tn * 16 + e * 4) * 4, v);
+          for (int j = 0; j < 4; ++j)
+            v[j] = a.zscale ? red[row * 16 + g * 4 + j] * a.zscale[n0 + g * 4 + j]
+                            : red[row * 16 + g * 4 + j];
+          store_coherent4(rz, (int)(((int64_t)(r0 + row) * R3 + n0 + g * 4) * 4), v);
+        }
+      } else {
+        // the routing epilogue of these tokens; c into LDS, then published
+        float* ue = dyn;             // (E, r1)
+        float* cl = ue + E * R1;     // (16, r1)
+        if (threadIdx.x < E * R1) ue[threadIdx.x] = uev;
+        __syncthreads();
+        const int ln = threadIdx.x & 15, row = threadIdx.x >> 4;
+        if (row < rows)   // row-uniform
+          route_row16(a, r0 + row, ln, ln < E ? red[row * 16 + ln] : 0.f, ue, cl + row * R1);
+        __syncthreads();
+        for (int q = threadIdx.x; q < rows * R1; q += 64 * W)
+          store_coherent(sc.cs + r0 * R1 + q, cl[q]);
       }
-      sync_publish(a.sync + sync_flag(decode_slice_flag(NZ, S, blk, sl)), a.epoch);
-      return;
     }
-    if (S > 1) {
-      // the other slices' tiles, added in slice order, then this one's
-      const bool ok = sync_await(a.sync + sync_flag(decode_slice_flag(NZ, S, blk, 0)), S - 1,
-                                 a.epoch, a.sync, reinterpret_cast<int*>(red + MF * 256), true);
-      for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
-        f32x4 pv[3];   // S <= 4: every load issued before the first is used
-#pragma unroll
-        for (int q = 0; q < 3; ++q)
-          pv[q] = q < S - 1 ? load_coherent4(rp, ((blk * (S - 1) + q) * Tn * 16 + e * 4) * 4)
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
-        f32x4 v = pv[0];
-#pragma unroll
-        for (int q = 1; q < 3; ++q)
-          if (q < S - 1) v += pv[q];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) red[e * 4 + j] = ok ? v[j] + red[e * 4 + j] : __builtin_nanf("");
-      }
-      __syncthreads();
-    }
-    if (blk < NZ) {
-      // z columns (scaled: fp8 plans), four to a store
-      const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
-      for (int e = threadIdx.x; e < Tn * 4; e += 64 * W) {
-        const int row = e >> 2, g = e & 3;
-        f32x4 v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          v[j] = a.zscale ? red[row * 16 + g * 4 + j] * a.zscale[n0 + g * 4 + j]
-                          : red[row * 16 + g * 4 + j];
-        store_coherent4(rz, (int)(((int64_t)row * R3 + n0 + g * 4) * 4), v);
-      }
-    } else {
-      // the routing epilogue of every token; c into LDS, then published
-      float* ue = dyn;             // (E, r1)
-      float* cl = ue + E * R1;     // (MF 16, r1)
-      if (threadIdx.x < E * R1) ue[threadIdx.x] = uev;
-      __syncthreads();
-      const int ln = threadIdx.x & 15;
-      for (int t = threadIdx.x >> 4; t < Tn; t += 4 * W)   // row-uniform
-        route_row16(a, t, ln, ln < E ? red[t * 16 + ln] : 0.f, ue, cl + t * R1);
-      __syncthreads();
-      for (int q = threadIdx.x; q < Tn * R1; q += 64 * W) store_coherent(sc.cs + q, cl[q]);
-    }
-    sync_publish(a.sync + sync_flag(blk), a.epoch);
+    sync_publish(a.sync + sync_flag(bid), a.epoch);
     return;
   }
   // ---- consumers: 16 columns of out = (c (x) z) W^T + bias ----
@@ -755,7 +716,7 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) gv[j][q] = g < NG ? a.gain[col + q] : 0.f;
   }
-  const bool ok = sync_await(a.sync + sync_flag(0), NZ + 1, a.epoch, a.sync,
+  const bool ok = sync_await(a.sync + sync_flag(0), NP, a.epoch, a.sync,
                              reinterpret_cast<int*>(red), false);
   // every load first: the z groups and c
   const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
