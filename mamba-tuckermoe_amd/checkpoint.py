@@ -11,7 +11,12 @@
                       {pfx}.ls_out_proj.gamma                       (weights.py:43-56)
    load_npz reads it with numpy's default loader (no pickles); load_layer,
    load_ffn and load_out_proj fill this package's modules from those keys and
-   refresh their packed copies.
+   refresh their packed copies. export_npz writes such a file: every floating
+   tensor of a state dict (or of a module, or of a torch checkpoint holding one
+   under "model" or "state_dict") as a float32 array under its key, the export
+   step of sft_cot_bundle/scripts/export/export_ckpt_to_npz.py:24-66. Checkpoint
+   files are read with torch.load(weights_only=True) only: a file that needs
+   unpickling of arbitrary objects is refused.
 
 2. The packed file (no counterpart in the reference) holds one TuckerMoE: its
    parameters under the reference's keys (so that it re-derives everything), fp8
@@ -42,6 +47,40 @@ def load_npz(path: str) -> Dict[str, np.ndarray]:
     """The arrays of a reference checkpoint (np.load without pickles)."""
     with np.load(path, allow_pickle=False) as z:
         return {k: z[k] for k in z.files}
+
+
+def checkpoint_state_dict(obj) -> Dict[str, torch.Tensor]:
+    """The tensors of a checkpoint object: obj["model"], else obj["state_dict"], else
+    obj itself when it is a dict; non-tensor entries are dropped
+    (export_ckpt_to_npz.py:24-40). A torch.nn.Module gives its state_dict()."""
+    if isinstance(obj, torch.nn.Module):
+        obj = obj.state_dict()
+    if not isinstance(obj, dict):
+        raise TypeError(f"no state dict in a {type(obj).__name__}")
+    raw = obj.get("model", obj.get("state_dict", obj))
+    if isinstance(raw, torch.nn.Module):
+        raw = raw.state_dict()
+    if not isinstance(raw, dict):
+        raise TypeError("the checkpoint's state dict is not a dict")
+    return {str(k): v for k, v in raw.items() if torch.is_tensor(v)}
+
+
+def export_npz(src, path: str, prefix: str = "", compressed: bool = True) -> int:
+    """Writes the floating tensors of src (a state dict, a module, a checkpoint
+    dict, or the path of a torch checkpoint file, read with weights_only=True) to
+    the .npz at path as float32 arrays (bf16 / fp16 widened exactly), each key
+    prefixed with `prefix` (e.g. "backbone.layers.0.block.ffn.gate_proj." for one
+    layer's own state dict). Integer tensors (fp8 codes) keep their dtype. Returns
+    the number of arrays written (export_ckpt_to_npz.py:43-66)."""
+    if isinstance(src, (str, bytes)) or hasattr(src, "__fspath__"):
+        src = torch.load(src, map_location="cpu", weights_only=True)
+    sd = checkpoint_state_dict(src)
+    arrays = {}
+    for k, t in sd.items():
+        t = t.detach().cpu()
+        arrays[prefix + k] = (t.float() if t.is_floating_point() else t).numpy()
+    (np.savez_compressed if compressed else np.savez)(path, **arrays)
+    return len(arrays)
 
 
 def load_layer(moe: TuckerMoE, arrays: Dict, pfx: str) -> None:

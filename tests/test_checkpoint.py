@@ -89,3 +89,44 @@ def test_packed_file_metadata_checks(pkg, tmp_path):
 
 def test_packed_layout_version_exported(pkg):
     assert pkg._lib.lib().tmoe_packed_layout_version() >= 3
+
+
+def test_export_npz_round_trip(pkg, tmp_path):
+    """export_npz (the .pt -> .npz step, export_ckpt_to_npz.py:43-66): a bf16 layer's
+    state dict, saved as a torch checkpoint under "model" with a non-tensor entry
+    beside it, comes back through load_npz / load_layer bit-exactly; bf16 widens to
+    float32 exactly."""
+    w = pkg.Workload("x", 8, 64, 96, 4, 2, 2, 64, 64, torch.float32, 21)
+    lp = pkg.synth.make_params(w, affine="random")
+    src = pkg.TuckerMoE(64, 96, w.cfg()).to(torch.bfloat16)
+    src.load_state_dict({k: v.to(torch.bfloat16) for k, v in lp.items()})
+    pfx = "backbone.layers.2.block.ffn.up_proj"
+    ckpt = tmp_path / "ckpt.pt"
+    torch.save({"model": src.state_dict(), "step": 40, "note": "sft"}, ckpt)
+    n = pkg.checkpoint.export_npz(str(ckpt), str(tmp_path / "w.npz"), prefix=pfx + ".")
+    assert n == len(src.state_dict())
+    arrays = pkg.checkpoint.load_npz(str(tmp_path / "w.npz"))
+    assert set(arrays) == {f"{pfx}.{k}" for k in src.state_dict()}
+    assert all(a.dtype == np.float32 for a in arrays.values())
+    dst = pkg.TuckerMoE(64, 96, w.cfg()).to(torch.bfloat16)
+    pkg.checkpoint.load_layer(dst, arrays, pfx)
+    for k, v in src.state_dict().items():
+        assert torch.equal(dst.state_dict()[k], v), k
+    # a module and a plain dict give the same arrays
+    pkg.checkpoint.export_npz(src, str(tmp_path / "m.npz"), prefix=pfx + ".")
+    again = pkg.checkpoint.load_npz(str(tmp_path / "m.npz"))
+    assert all(np.array_equal(again[k], arrays[k]) for k in arrays)
+
+
+class _Opaque:
+    pass
+
+
+def test_export_npz_refuses_pickled_objects(pkg, tmp_path):
+    """Checkpoint files are read with weights_only=True: one holding an arbitrary
+    Python object is refused, not unpickled."""
+    path = tmp_path / "bad.pt"
+    torch.save({"model": {"w": torch.ones(2)}, "obj": _Opaque()}, path)
+    with pytest.raises(Exception):
+        pkg.checkpoint.export_npz(str(path), str(tmp_path / "o.npz"))
+    assert not (tmp_path / "o.npz").exists()
