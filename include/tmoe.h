@@ -176,8 +176,15 @@ int tmoe_pack_weights_fp8(const tmoe_plan* plan, const void* router_w,
  *   topk_w   (T, k) f32, nullable: the routing weights (mode 0: softmax over the k
  *            selected logits, model.py:77)
  *   logits   (T, E) f32, nullable: router scores x @ router_w^T (model.py:75)
- *   workspace of at least tmoe_workspace_bytes(plan, T) bytes.
- * T == 0 is a no-op. Stream-ordered, no allocation, no host synchronisation. */
+ *   workspace of at least tmoe_workspace_bytes(plan, T) bytes. Its contents need
+ *            no initialisation: kernels whose work-groups hand data to each other
+ *            inside one launch (the T <= 64 bf16 decode launch, the E = 256 front)
+ *            tag their signal words with a value drawn per launch, and wait at most
+ *            20 ms for one (past that the affected rows come out NaN; the launch
+ *            still completes).
+ * T == 0 is a no-op. Stream-ordered, no allocation, no host synchronisation. Under
+ * HIP graph capture the decode-size batches take the two-launch path (the one-launch
+ * kernel's signal words would read as already set on a replay). */
 int tmoe_forward(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
                  void* out, int32_t* topk_idx, float* topk_w, float* logits,
                  void* workspace, size_t workspace_bytes, void* stream);
