@@ -30,6 +30,8 @@ struct tmoe_plan {
   size_t off_sin, off_cscale, off_sout, off_craw, packed_bytes;
   bool core_p;      // the core runs k_core_pp (T > kSmallT) from P^T at off_core_p
   size_t off_core_p;
+  bool wfrag;       // the front operand also in k_front_ks's fragment order, at off_wfrag
+  size_t off_wfrag;
   // rank of the contraction the kernels run: r1, or E for plans packed in the
   // expert form (fewer experts than ranks, weights not fp8): U_expert packed as
   // the identity (E x E) and core as G_e = sum_r U_expert[e, r] core_r
@@ -147,6 +149,7 @@ tmoe::FwdArgs make_args(const tmoe_plan* p, const void* x, int64_t T, const void
   a.r1 = p->rk; a.r2 = s.r2; a.r3 = s.r3; a.eps = s.eps;
   a.x = x;
   a.wfront = pk + p->off_front;
+  a.wfrag = p->wfrag ? pk + p->off_wfrag : nullptr;
   a.gain = reinterpret_cast<const float*>(pk + p->off_gain);
   a.uexp = reinterpret_cast<const float*>(pk + p->off_uexp);
   a.coreT = pk + p->off_core;
@@ -322,6 +325,13 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
   if (p->core_p) { p->off_core_p = o; o = align256(o + (size_t)p->rk * s.r2 * s.r3 * p->es); }
   p->off_fold = 0;
   if (p->fold) { p->off_fold = o; o = align256(o + (size_t)s.d_out * K * p->es); }
+  // the register-weight front (k_front_ks): bf16 kernels, r3 = 256, one router block
+  p->wfrag = bf && s.r3 == 256 && p->E_pad == 32;
+  p->off_wfrag = 0;
+  if (p->wfrag) {
+    p->off_wfrag = o;
+    o = align256(o + (size_t)(s.r3 + p->E_pad) * s.d_in * p->es);
+  }
   p->packed_bytes = o;
   *plan_out = p;
   return TMOE_OK;
@@ -338,8 +348,9 @@ int tmoe_plan_folded(const tmoe_plan* plan) { return plan && plan->fold ? 1 : 0;
 // 1: front operand, gain, U_expert, core^T, U_out^T, bias, fp8 tables; 2: + P^T for
 // r1 in {1, 2, 4}; 3: P^T also for r1 = 4G in rank-group order; 4: plans with fewer
 // experts than ranks packed in the expert form (identity U_expert, core G); 5: folded
-// plans add W^T = (core U_out)^T.
-int tmoe_packed_layout_version(void) { return 6; }
+// plans add W^T = (core U_out)^T; 7: bf16 plans with r3 = 256 and E_pad = 32 add the
+// front operand in fragment order (k_front_ks).
+int tmoe_packed_layout_version(void) { return 7; }
 
 size_t tmoe_workspace_bytes(const tmoe_plan* plan, int64_t T) {
   if (!plan || T < 0) return 0;
@@ -372,6 +383,9 @@ int tmoe_pack_weights(const tmoe_plan* p, const void* router_w, const void* U_in
   if ((e = tmoe::launch_copy_pad(router_w, base + p->off_router, s.E * s.d_in,
                                  p->E_pad * s.d_in, es, st)) != hipSuccess)
     return hip_fail(e, "pack router");
+  if (p->wfrag && (e = tmoe::launch_pack_frag(base + p->off_front, base + p->off_wfrag,
+                                              s.r3 + p->E_pad, s.d_in, st)) != hipSuccess)
+    return hip_fail(e, "pack front fragments");
   if ((e = tmoe::launch_to_f32(inner_w, reinterpret_cast<float*>(base + p->off_gain), s.r3,
                                s.dtype, st)) != hipSuccess)
     return hip_fail(e, "pack inner_norm.weight");
@@ -442,6 +456,9 @@ int tmoe_pack_weights_fp8(const tmoe_plan* p, const void* router_w, const uint8_
   if ((e = tmoe::launch_copy_pad(router_w, base + p->off_router, s.E * s.d_in,
                                  p->E_pad * s.d_in, 2, st)) != hipSuccess)
     return hip_fail(e, "pack router");
+  if (p->wfrag && (e = tmoe::launch_pack_frag(base + p->off_front, base + p->off_wfrag,
+                                              s.r3 + p->E_pad, s.d_in, st)) != hipSuccess)
+    return hip_fail(e, "pack front fragments");
   if ((e = tmoe::launch_to_f32(inner_w, f32at(p->off_gain), s.r3, TMOE_BF16, st)) != hipSuccess)
     return hip_fail(e, "pack inner_norm.weight");
   if ((e = tmoe::launch_to_f32(U_expert, f32at(p->off_uexp), s.E * s.r1, TMOE_BF16, st)) !=

@@ -34,6 +34,8 @@ struct FwdArgs {
   // packed weights
   const void* wfront;           // (r3 + E_pad, d_in)   U_in^T rows, then router rows
                                 //                      (zero rows past E)
+  const void* wfrag;            // wfront in k_front_ks's fragment order (bf16 plans
+                                //                      with r3 = 256, E_pad = 32), else null
   const float* gain;            // (r3)                 inner_norm.weight
   const float* uexp;            // (E, r1)              U_expert
   const void* coreT;            // (r2, r1*r3)          core as (r1*r3, r2), transposed
@@ -229,6 +231,9 @@ hipError_t launch_transpose_e4m3(const uint8_t* src, uint16_t* dst, int64_t rows
 // k_core_pp's P^T (r1*r2, r3) from core (r1, r3, r2), or with src_t from core^T
 // (r2, r1*r3): bf16 bits, or e4m3 codes with channel scales sc (r1, r2) (null for
 // bf16; a zero scale packs its channel as zeros).
+// k_front_ks's fragment order of the packed front operand (rows % 32 == 0)
+hipError_t launch_pack_frag(const void* wfront, void* dst, int64_t rows, int64_t d_in,
+                            hipStream_t stream);
 hipError_t launch_pack_core_p(const void* core, bool e4m3, const float* sc, uint16_t* dst,
                               int64_t r1, int64_t r3, int64_t r2, hipStream_t stream,
                               bool src_t = false);

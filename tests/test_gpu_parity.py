@@ -101,6 +101,19 @@ def test_wide_outproj_ragged(pkg, dev, T, fold):
     _check(w, got, onp.forward_f64(x, params, w.k), f"C3/T={T}/fold={fold}")
 
 
+# The register-weight front (k_front_ks: bf16, r3 = 256, E_pad = 32, T past one round
+# of 32-token tiles): E = 24, k = 3, d_in of 17 K tiles (the K loop's ring tail), a
+# ragged last tile, both forms.
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+def test_register_weight_front(pkg, dev, fold):
+    w = pkg.Workload("custom", 9000 - 7, 1088, 288, 24, 3, 4, 256, 256, torch.bfloat16, 81)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    m = _module(pkg, dev, w, params, fold)
+    got = _run(m, x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"ks-front/fold={fold}")
+
+
 # Mid-size T: the 128 x 144-tile out-projection (k_outproj_mid, T <= 2048 at the C3
 # shapes) and the 128 x 288 tiles of k_outproj_wide<1> (2048 < T <= 4096): ragged
 # last row tiles, a K of 256 and two column tiles.
