@@ -1232,7 +1232,7 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
     const int row = inb ? row_raw : BM - 1;   // lanes past the tile repeat its last row
     const bool live = inb && row < rows_valid;
     const int64_t g = m0 + row;
-    uint64_t key[PL];   // 0 for columns past E and for taken candidates
+    uint64_t key[PL];   // 0 for columns past E
     float sv[PL];       // the scores the keys rank (router_mode 1: capped ones)
 #pragma unroll
     for (int p = 0; p < PL; ++p) {
@@ -1245,17 +1245,24 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
       key[p] = col < E ? rank_key(sv[p], col) : 0;
     }
     float vmax = 0.f, ssum = 0.f;
+    // round kk takes the largest key below the one round kk - 1 took (keys are
+    // distinct: they hold the column), so no key is cleared between the rounds
+    uint64_t prev = 0;
 #pragma unroll 1
     for (int kk = 0; kk < K; ++kk) {
       uint64_t best = 0;
+      if (kk == 0) {
 #pragma unroll
-      for (int p = 0; p < PL; ++p) best = key[p] > best ? key[p] : best;
+        for (int p = 0; p < PL; ++p) best = key[p] > best ? key[p] : best;
+      } else {
+#pragma unroll
+        for (int p = 0; p < PL; ++p) best = key[p] < prev && key[p] > best ? key[p] : best;
+      }
       group_max_key<G>(best);
+      prev = best;
       // k <= E, so a candidate always remains: best > 0 and its index is < E
       const int bi = key_index(best);
       const float bv = key_value(best);
-#pragma unroll
-      for (int p = 0; p < PL; ++p) key[p] = key[p] == best ? 0 : key[p];
       if (kk == 0) vmax = bv;   // the largest
       const float ex = expf(bv - vmax);
       ssum += ex;
