@@ -1241,9 +1241,16 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
 #pragma unroll
       for (int w = 0; w < NP; ++w) sc += lg[(w * BM + row) * LD + col];
       if (a.logits && live && col < E) a.logits[g * E + col] = sc;
-      sv[p] = mode ? capped_score(sc, a.router_scale, a.router_temperature) : sc;
-      key[p] = col < E ? rank_key(sv[p], col) : 0;
+      sv[p] = sc;
     }
+    // a branch on the uniform mode: selected per key, the capped score's exp and
+    // divisions ran for every key in mode 0 as well
+    if (mode) {
+#pragma unroll
+      for (int p = 0; p < PL; ++p) sv[p] = capped_score(sv[p], a.router_scale, a.router_temperature);
+    }
+#pragma unroll
+    for (int p = 0; p < PL; ++p) key[p] = gl + G * p < E ? rank_key(sv[p], gl + G * p) : 0;
     float vmax = 0.f, ssum = 0.f;
     // round kk takes the largest key below the one round kk - 1 took (keys are
     // distinct: they hold the column), so no key is cleared between the rounds

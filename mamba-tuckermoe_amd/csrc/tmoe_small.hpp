@@ -312,9 +312,14 @@ __device__ __forceinline__ void epi_finish(const FwdArgs& a, int64_t t, int lane
     const int e = lane + 64 * q;
     const float lv = e < E ? L.lr[q] : 0.f;
     if (routing && a.logits && e < E) a.logits[t * E + e] = lv;
-    sv[q] = mode ? capped_score(lv, a.router_scale, a.router_temperature) : lv;
-    key[q] = e < E ? rank_key(sv[q], e) : 0;
+    sv[q] = lv;
   }
+  if (mode) {   // a uniform branch (selected, the exp and divisions ran in mode 0 too)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sv[q] = capped_score(sv[q], a.router_scale, a.router_temperature);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) key[q] = lane + 64 * q < E ? rank_key(sv[q], lane + 64 * q) : 0;
   // K rounds of a wave max-key; lane kk keeps round kk's winner (K <= 16 < 64)
   float selv = 0.f;
   int si = 0;
@@ -582,7 +587,8 @@ __device__ __forceinline__ void route_row16(const FwdArgs& a, int64_t t, int sl,
   const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
   const int mode = a.router_mode;
   if (a.logits && sl < E) a.logits[t * E + sl] = lv;
-  const float sv = mode ? capped_score(lv, a.router_scale, a.router_temperature) : lv;
+  float sv = lv;
+  if (mode) sv = capped_score(lv, a.router_scale, a.router_temperature);   // uniform branch
   uint64_t key = sl < E ? rank_key(sv, sl) : 0;
   float selv = 0.f, vmax = 0.f;
   int si = 0;
