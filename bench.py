@@ -313,6 +313,8 @@ def main():
                     help="time the FFN sub-block of this FFN workload (F0, F1, F2) instead")
     ap.add_argument("--no-fold", action="store_true",
                     help="keep the core and the out-projection as two GEMMs (TMOE_FLAG_NO_FOLD)")
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="never run the large-T forward as one launch (TMOE_FLAG_NO_FUSE)")
     ap.add_argument("--latent", action="store_true",
                     help="time FusedLatentMoE forward + backward (training path) instead")
     args = ap.parse_args()
@@ -362,6 +364,7 @@ def main():
     m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
     m.load_state_dict({k: v.to(dev) for k, v in params.items()})
     m.set_fold(not args.no_fold)
+    m.set_fuse(not args.no_fuse)
     if codes is not None:
         m.load_fp8(*[codes[k].to(dev) for k in ("U_in_q", "U_in_scale", "core_q", "core_scale",
                                                   "U_out_q", "U_out_scale")])

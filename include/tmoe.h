@@ -33,13 +33,15 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 9
+#define TMOE_ABI_VERSION 10
 
 /* error codes */
 #define TMOE_OK            0
 #define TMOE_EINVAL       -1  /* bad argument: null/misaligned pointer, bad size     */
 #define TMOE_EUNSUPPORTED -2  /* valid for the reference, not supported by a kernel */
 #define TMOE_EHIP         -3  /* a HIP runtime call failed                           */
+#define TMOE_ESIGNAL      -4  /* an earlier forward's kernel recorded a lost in-launch
+                                 signal (tmoe_signal_status)                          */
 
 /* element types */
 #define TMOE_F32  0
@@ -68,6 +70,8 @@ extern "C" {
  * must be > 0 (unused in mode 0). */
 /* plan flags (tmoe_shape.flags) */
 #define TMOE_FLAG_NO_FOLD 1  /* keep the core and the out-projection as two GEMMs */
+#define TMOE_FLAG_NO_FUSE 2  /* never run the large-T forward as one launch (see
+                                tmoe_forward): front and out-projection as two */
 
 typedef struct tmoe_shape {
   int64_t d_in, d_out;
@@ -178,13 +182,21 @@ int tmoe_pack_weights_fp8(const tmoe_plan* plan, const void* router_w,
  *   logits   (T, E) f32, nullable: router scores x @ router_w^T (model.py:75)
  *   workspace of at least tmoe_workspace_bytes(plan, T) bytes. Its contents need
  *            no initialisation: kernels whose work-groups hand data to each other
- *            inside one launch (the T <= 64 bf16 decode launch, the E = 256 front)
- *            tag their signal words with a value drawn per launch, and wait at most
- *            20 ms for one (past that the affected rows come out NaN; the launch
- *            still completes).
+ *            inside one launch (the T <= 64 bf16 decode launch, the E = 256 front,
+ *            the one-launch large-T forward) tag their signal words with a value
+ *            drawn per launch, and wait for one at most a budget of polls
+ *            (tmoe_set_wait_polls; about a second by default). Past it the affected
+ *            rows come out NaN (or stale), the launch still completes, and the
+ *            plan's status records it: tmoe_signal_status reports TMOE_ESIGNAL.
+ * The large-T forward of a folded bf16 plan with r3 = 256, E <= 32 and d_out a
+ * multiple of 288 runs as one launch (front and out-projection in one persistent
+ * grid, one work-group per compute unit) on a 256-compute-unit device when its
+ * 256 x 288 output tiles number at least 256 (T >= 8192 at d_out = 2304), unless
+ * the plan has TMOE_FLAG_NO_FUSE.
  * T == 0 is a no-op. Stream-ordered, no allocation, no host synchronisation. Under
- * HIP graph capture the decode-size batches take the two-launch path (the one-launch
- * kernel's signal words would read as already set on a replay). */
+ * HIP graph capture the kernels whose signal flags have several consumers are not
+ * used (their flags would read as already set on a replay): decode-size batches,
+ * the large-T forward and the E = 256 front take their multi-launch paths. */
 int tmoe_forward(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
                  void* out, int32_t* topk_idx, float* topk_w, float* logits,
                  void* workspace, size_t workspace_bytes, void* stream);
@@ -224,12 +236,35 @@ int tmoe_forward_epi(const tmoe_plan* plan, const void* x, int64_t T, const void
  * process ends; this call allocates nothing. T whose workspace
  * (tmoe_workspace_bytes) exceeds it gives TMOE_EUNSUPPORTED before any GPU work.
  * All calls on one GPU share that GPU's array: calls that overlap on one GPU (on
- * different streams, or from different threads without ordering) race. Arguments,
- * results and errors otherwise as tmoe_forward; not recorded by tmoe_prof_*. */
+ * different streams, or from different threads without ordering) race. The array
+ * used is that of the device `stream` belongs to (the current device for the null
+ * stream). Arguments, results and errors otherwise as tmoe_forward; not recorded by
+ * tmoe_prof_*. */
 size_t tmoe_static_scratch_bytes(void);
 int tmoe_forward_static(const tmoe_plan* plan, const void* x, int64_t T, const void* packed,
                         void* out, int32_t* topk_idx, float* topk_w, float* logits,
                         void* stream);
+
+/* Lost in-launch signals. No counterpart in the reference (its forward has no
+ * kernels that wait for each other; torch raises its errors from the call).
+ * A kernel whose wait for another work-group of its launch runs out of its poll
+ * budget sets a word of the plan's status block (pinned host memory the kernels
+ * write directly; allocated by tmoe_plan_create when a GPU is present).
+ * tmoe_signal_status reads it without synchronising: it reflects the kernels of
+ * this plan that have completed. For a definitive answer about a forward,
+ * synchronise its stream first. Returns TMOE_OK, or TMOE_ESIGNAL with *mask
+ * (nullable) holding the TMOE_STATUS_* bits; clear != 0 resets the block. Rows
+ * affected by a lost signal are NaN or stale; nothing else of the forward is. */
+#define TMOE_STATUS_SIGNAL    1u  /* a wait ran out of its poll budget */
+int tmoe_signal_status(const tmoe_plan* plan, int clear, uint32_t* mask);
+
+/* Sets the budget of every in-launch wait of later forwards, in polls of the
+ * awaited flags (default 1000000, about a second), process-wide; returns the
+ * previous budget. polls < 0 only returns it. A budget of 0 makes every wait give
+ * up without looking at its flags, so that the lost-signal path can be exercised
+ * with every kernel still exiting normally (its forwards then produce NaN rows and
+ * TMOE_ESIGNAL). No counterpart in the reference. */
+int64_t tmoe_set_wait_polls(int64_t polls);
 
 /* out = R(R(silu(gate(x))) * up(x)) for two layers of one plan over the same input:
  * F.silu(ffn_gate(x_f)) * ffn_up(x_f) of model.py:338-340, i.e. tmoe_forward of the

@@ -42,17 +42,17 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles every source and links libtmoe.so; returns its path."""
+    """Compiles every source (concurrently) and links libtmoe.so; returns its path."""
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
+    objs, cmds = [], []
     for src in SOURCES:
         obj = os.path.join(objdir, src + ".o")
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c",
-               os.path.join(CSRC, src), "-o", obj]
-        _run(cmd, verbose)
+        cmds.append([hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c",
+                     os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
+    _run_all(cmds, verbose)
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
            "-Wl,-rpath,/opt/rocm/lib"]
@@ -61,13 +61,35 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+# hipcc's host pass does not know the packed-fp32 feature and says so: harmless.
+_NOISE = "'-packed-fp32-ops' is not a recognized feature"
+
+
+def _run_all(cmds, verbose):
+    """Runs the compile commands side by side; raises on the first that failed."""
+    procs = []
+    for cmd in cmds:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                            text=True)))
+    failed = None
+    for cmd, pr in procs:
+        _, stderr = pr.communicate()
+        err = "\n".join(l for l in stderr.splitlines() if _NOISE not in l)
+        if pr.returncode != 0 and failed is None:
+            failed = f"build failed ({pr.returncode}): {' '.join(cmd)}\n{err}"
+        elif verbose and err.strip():
+            print(err)
+    if failed:
+        raise RuntimeError(failed)
+
+
 def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass does not know the packed-fp32 feature and says so: harmless.
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in res.stderr.splitlines() if _NOISE not in l)
     if res.returncode != 0:
         raise RuntimeError(f"build failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():

@@ -19,12 +19,14 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 9
-TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP = 0, -1, -2, -3
+ABI_VERSION = 10
+TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP, TMOE_ESIGNAL = 0, -1, -2, -3, -4
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
 TMOE_EPI_NONE, TMOE_EPI_GLU, TMOE_EPI_RESIDUAL_SCALE = 0, 1, 2
 TMOE_FLAG_NO_FOLD = 1
+TMOE_FLAG_NO_FUSE = 2
+TMOE_STATUS_SIGNAL = 1
 TMOE_LATENT_P_F32 = 0x100   # or'ed into a latent call's dtype: p and dp are fp32
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
@@ -38,6 +40,7 @@ EXPORTED = (
     "tmoe_forward", "tmoe_forward_epi", "tmoe_forward_glu", "tmoe_rmsnorm_rows",
     "tmoe_static_scratch_bytes", "tmoe_forward_static",
     "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
+    "tmoe_signal_status", "tmoe_set_wait_polls",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
 
@@ -124,6 +127,10 @@ def lib() -> ctypes.CDLL:
         L.tmoe_latent_backward.restype = ctypes.c_int
         L.tmoe_latent_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
                                            ctypes.c_int, vp, vp, vp, vp, sz, vp]
+        L.tmoe_signal_status.restype = ctypes.c_int
+        L.tmoe_signal_status.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint32)]
+        L.tmoe_set_wait_polls.restype = ctypes.c_int64
+        L.tmoe_set_wait_polls.argtypes = [i64]
         L.tmoe_prof_enable.restype = ctypes.c_int
         L.tmoe_prof_enable.argtypes = [ctypes.c_int]
         L.tmoe_prof_read.restype = ctypes.c_int
@@ -199,10 +206,24 @@ class Plan:
         """True if the forward runs one GEMM of c (x) z against W = core U_out."""
         return bool(lib().tmoe_plan_folded(self._ptr))
 
+    def signal_status(self, clear: bool = True) -> int:
+        """The TMOE_STATUS_* bits that completed kernels of this plan's forwards set
+        (tmoe_signal_status; reads host memory, no synchronisation). Raises TmoeError
+        (code TMOE_ESIGNAL) when any is set; clears them first when `clear`."""
+        mask = ctypes.c_uint32()
+        check(lib().tmoe_signal_status(self._ptr, 1 if clear else 0, ctypes.byref(mask)))
+        return int(mask.value)
+
     def __del__(self):
         ptr, self._ptr = getattr(self, "_ptr", None), None
         if ptr and getattr(self, "_destroy", None):
             self._destroy(ptr)
+
+
+def set_wait_polls(polls: int) -> int:
+    """Budget of the kernels' in-launch waits, in polls (process-wide); returns the
+    previous one. 0 makes every wait give up at once (the lost-signal test hook)."""
+    return int(lib().tmoe_set_wait_polls(int(polls)))
 
 
 def prof_enable(on: bool) -> None:

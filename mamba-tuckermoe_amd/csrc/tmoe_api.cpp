@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -39,6 +40,10 @@ struct tmoe_plan {
   // folded form (large T): W^T (d_out, rk*r3) at off_fold, one GEMM of c (x) z against W
   bool fold;
   size_t off_fold;
+  // status block (tmoe::kStatusWords words of pinned host memory mapped for the
+  // device, set by kernels; null on a machine without a GPU): host and device address
+  uint32_t* status_host;
+  uint32_t* status_dev;
 };
 
 namespace {
@@ -58,6 +63,39 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// budget of the kernels' waits for in-launch signals, in polls (tmoe_set_wait_polls)
+std::atomic<int> g_wait_polls{tmoe::kDefaultWaitPolls};
+
+// The plan's status block: pinned host memory the kernels write through a mapped
+// device address. Left null when no GPU is present (plans stay usable for every
+// host-side call) or when the allocation fails (the kernels then report only
+// through the workspace's error word).
+void alloc_status(tmoe_plan* p) {
+  p->status_host = p->status_dev = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();   // leave no sticky error behind
+    return;
+  }
+  void* h = nullptr;
+  if (hipHostMalloc(&h, tmoe::kStatusWords * sizeof(uint32_t),
+                    hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) !=
+          hipSuccess ||
+      !h) {
+    (void)hipGetLastError();
+    return;
+  }
+  memset(h, 0, tmoe::kStatusWords * sizeof(uint32_t));
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || !d) {
+    (void)hipGetLastError();
+    (void)hipHostFree(h);
+    return;
+  }
+  p->status_host = static_cast<uint32_t*>(h);
+  p->status_dev = static_cast<uint32_t*>(d);
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -175,6 +213,8 @@ tmoe::FwdArgs make_args(const tmoe_plan* p, const void* x, int64_t T, const void
   a.core_split = L.split;
   a.front_split = L.fsplit;
   a.sync = reinterpret_cast<uint32_t*>(ws + L.sync);
+  a.wait_polls = g_wait_polls.load(std::memory_order_relaxed);
+  a.status = p->status_dev;
   return a;
 }
 
@@ -193,12 +233,13 @@ hipError_t pack_fold(const tmoe_plan* p, char* base, hipStream_t st) {
 
 // A folded plan's large-T stages 2 and 3: c (x) z into mid, then the out-projection
 // kernel as one GEMM of width rk*r3 against W.
-tmoe::FwdArgs folded_args(const tmoe_plan* p, const tmoe::FwdArgs& a, const void* packed) {
+tmoe::FwdArgs folded_args(const tmoe_plan* p, const tmoe::FwdArgs& a, const void* packed,
+                          hipStream_t st) {
   tmoe::FwdArgs f = a;
   f.r2 = p->rk * p->s.r3;
   f.uoutT = static_cast<const char*>(packed) + p->off_fold;
   f.out_scale = nullptr;
-  f.cz = tmoe::front_fuses_cz(f) ? f.mid : nullptr;
+  f.cz = tmoe::front_fuses_cz(f, st) ? f.mid : nullptr;
   return f;
 }
 
@@ -277,7 +318,7 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     return fail(TMOE_EUNSUPPORTED, "top_k=%lld: at most %d", (long long)s.k, tmoe::kMaxTopK);
   if (s.r1 > 64)
     return fail(TMOE_EUNSUPPORTED, "r1=%lld: at most 64", (long long)s.r1);
-  if (s.flags & ~TMOE_FLAG_NO_FOLD)
+  if (s.flags & ~(TMOE_FLAG_NO_FOLD | TMOE_FLAG_NO_FUSE))
     return fail(TMOE_EINVAL, "flags 0x%x: unknown bits", (unsigned)s.flags);
   // a GEMM tile (at most 512 operand rows of at most 4 MB) spans < 4 GB: the
   // kernels address it with 32-bit offsets
@@ -333,11 +374,16 @@ int tmoe_plan_create(const tmoe_shape* shape, tmoe_plan** plan_out) {
     o = align256(o + (size_t)(s.r3 + p->E_pad) * s.d_in * p->es);
   }
   p->packed_bytes = o;
+  alloc_status(p);
   *plan_out = p;
   return TMOE_OK;
 }
 
-void tmoe_plan_destroy(tmoe_plan* plan) { delete plan; }
+void tmoe_plan_destroy(tmoe_plan* plan) {
+  if (!plan) return;
+  if (plan->status_host) (void)hipHostFree(plan->status_host);
+  delete plan;
+}
 
 size_t tmoe_packed_bytes(const tmoe_plan* plan) { return plan ? plan->packed_bytes : 0; }
 
@@ -534,10 +580,13 @@ int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool small = T <= tmoe::kSmallT;
   const bool fold = p->fold;
-  if (fold) a = folded_args(p, a, packed);
-  const Launch big_path[kStages] = {tmoe::launch_front,
-                                    fold ? launch_cz : tmoe::launch_core,
-                                    tmoe::launch_outproj};
+  if (fold) a = folded_args(p, a, packed, st);
+  // the large-T folded forward in one launch where the plan, T and the device allow
+  const bool fused = fold && !small && !(p->s.flags & TMOE_FLAG_NO_FUSE) &&
+                     tmoe::fused_large_ok(a, st);
+  const Launch big_path[kStages] = {fused ? tmoe::launch_fused_large : tmoe::launch_front,
+                                    fused ? launch_nothing : fold ? launch_cz : tmoe::launch_core,
+                                    fused ? launch_nothing : tmoe::launch_outproj};
   // folded: the out-projection builds c (x) z from z and c itself (no core stage)
   Launch small_path[kStages];
   small_stages(a, fold, st, small_path);
@@ -614,7 +663,7 @@ int tmoe_forward_static(const tmoe_plan* p, const void* x, int64_t T, const void
   if (!aligned16(x) || !aligned16(packed) || !aligned16(out))
     return fail(TMOE_EINVAL, "tmoe_forward_static: x/packed/out must be 16-byte aligned");
   void* ws = nullptr;
-  if (hipError_t e = tmoe::static_scratch(&ws); e != hipSuccess)
+  if (hipError_t e = tmoe::static_scratch(static_cast<hipStream_t>(stream), &ws); e != hipSuccess)
     return hip_fail(e, "tmoe_forward_static: static scratch address");
   return forward_impl(p, x, T, packed, out, topk_idx, topk_w, logits, ws,
                       tmoe::kStaticScratchBytes, TMOE_EPI_NONE, nullptr, nullptr, stream, false);
@@ -646,8 +695,8 @@ int tmoe_forward_glu(const tmoe_plan* p, const void* x, int64_t T, const void* p
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (p->fold) {
-    g = folded_args(p, g, packed_gate);
-    u = folded_args(p, u, packed_up);
+    g = folded_args(p, g, packed_gate, st);
+    u = folded_args(p, u, packed_up, st);
   }
   if (T <= tmoe::kSmallT) {
     for (const tmoe::FwdArgs* a : {&g, &u}) {
@@ -756,6 +805,28 @@ int tmoe_latent_backward(const void* x, const void* G, const int64_t* idx, const
   l.ws = workspace;
   const hipError_t e = tmoe::latent_backward(l, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_latent_backward");
+}
+
+int tmoe_signal_status(const tmoe_plan* plan, int clear, uint32_t* mask) {
+  g_err[0] = 0;
+  if (mask) *mask = 0;
+  if (!plan) return fail(TMOE_EINVAL, "tmoe_signal_status: null plan");
+  if (!plan->status_host) return TMOE_OK;   // no GPU: no kernel ever ran
+  volatile uint32_t* w = plan->status_host;
+  uint32_t m = 0;
+  if (w[tmoe::kStatusSignalWord]) m |= TMOE_STATUS_SIGNAL;
+  if (clear) w[tmoe::kStatusSignalWord] = 0;
+  if (mask) *mask = m;
+  if (!m) return TMOE_OK;
+  return fail(TMOE_ESIGNAL, "a kernel's wait for another work-group of its launch ran out of "
+                            "its poll budget (the affected output rows are NaN or stale)");
+}
+
+int64_t tmoe_set_wait_polls(int64_t polls) {
+  const int64_t prev = g_wait_polls.load(std::memory_order_relaxed);
+  if (polls >= 0) g_wait_polls.store(polls > INT32_MAX ? INT32_MAX : (int)polls,
+                                     std::memory_order_relaxed);
+  return prev;
 }
 
 int tmoe_prof_enable(int on) {

@@ -14,8 +14,9 @@ constexpr int kTileKBytes = 128;
 // Bytes of the static scratch of tmoe_forward_static (tmoe_static.hip): the
 // forward's workspace for up to T = 16384 tokens at the reference's C3 shape.
 constexpr size_t kStaticScratchBytes = (size_t)48 << 20;
-// Device address of the static scratch on the current GPU (looked up once per GPU).
-hipError_t static_scratch(void** ptr);
+// Device address of the static scratch on the GPU that `stream` belongs to (the
+// current GPU for the null stream), looked up once per GPU.
+hipError_t static_scratch(hipStream_t stream, void** ptr);
 
 constexpr int kFrontBM = 64;    // tokens per k_front work-group (whole r3 and E rows)
 constexpr int kFrontPFA = 8;    // K tiles of x in flight per k_front work-group
@@ -77,7 +78,21 @@ struct FwdArgs {
   // published, drawn fresh by the launcher (next_epoch)
   uint32_t* sync;
   uint32_t epoch;
+  // a wait for a flag gives up after this many polls (kDefaultWaitPolls unless the
+  // host set another budget; 0: at once), then sets word kStatusSignal of `status`
+  int wait_polls;
+  // the plan's status block in host-visible memory (words kStatus*, set to 1 by a
+  // kernel that met the condition; read by tmoe_signal_status), or null
+  uint32_t* status;
 };
+
+// Default budget of a wait for an in-launch signal, in polls of its flags (a poll is
+// a device-scope load round trip plus ~128 clocks of sleep: about a second in all)
+constexpr int kDefaultWaitPolls = 1000000;
+// words of a plan's status block (host memory mapped for the device): word
+// kStatusSignalWord is set when a wait ran out of polls (the others are spare)
+constexpr int kStatusWords = 4;
+constexpr int kStatusSignalWord = 0;
 
 // FwdArgs::sync: the error word, then one flag per 32-token tile of the largest T a
 // launch that signals may have, each flag alone in its 256-byte block (polls and
@@ -214,7 +229,13 @@ hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t stream);
 // Whether the large-T front kernel that launch_front picks for `a` can write c (x) z
 // itself (a.cz): the single-kind front (not the K-sliced one nor the split one of
 // the widest routers) with at most 32 ranks. Then no launch_expand_cz is needed.
-bool front_fuses_cz(const FwdArgs& a);
+bool front_fuses_cz(const FwdArgs& a, hipStream_t stream);
+// The whole large-T forward of a folded plan in one launch (k_fused_large): front
+// tiles and out-projection tiles in one persistent grid of one work-group per
+// compute unit, c (x) z handed over inside each XCD's L2. fused_large_ok: the plan,
+// T, the device and the stream allow it (f: the folded forward's arguments).
+bool fused_large_ok(const FwdArgs& f, hipStream_t stream);
+hipError_t launch_fused_large(const FwdArgs& f, hipStream_t stream);
 // small-T path: front = skinny GEMM + per-token epilogue; core; out-projection
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t stream);

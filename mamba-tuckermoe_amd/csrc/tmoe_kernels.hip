@@ -8,6 +8,7 @@
 #include "tmoe_outproj_wide.hpp"
 #include "tmoe_outproj_mid.hpp"
 #include "tmoe_front_ks.hpp"
+#include "tmoe_fused.hpp"
 
 namespace tmoe {
 namespace {
@@ -480,7 +481,37 @@ hipError_t launch_fold_out_t(const uint16_t* coreT, const uint16_t* uoutT, const
   return hipGetLastError();
 }
 
-bool front_fuses_cz(const FwdArgs& a) {
+// k_fused_large (tmoe_fused.hpp): a folded bf16 plan whose front is k_front_ks's
+// (r3 = 256, E_pad = 32, the fragment-order weights packed) and writes c (x) z,
+// whose out-projection is k_outproj_wide's (outproj_tiled_ok), with at least one
+// 256 x 288 tile per work-group (T >= 8192 at d_out = 2304), on a device of 256
+// compute units (8 XCDs of 32), with the workspace's signal words, and not under
+// graph capture (its flags have several consumers and stay set).
+bool fused_large_ok(const FwdArgs& a, hipStream_t st) {
+  if (a.dtype != kDtypeBF16 || !a.cz || !a.wfrag || a.r3 != 256 || a.E_pad != 32 || !a.sync)
+    return false;
+  if (!outproj_tiled_ok(a) || a.r2 % 64) return false;
+  const int64_t tiles = (int64_t)cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN);
+  if (tiles < dev::fused::kGrid || cu_count() != dev::fused::kGrid) return false;
+  // a signal flag per 64-token front tile, within the workspace's flags (one per
+  // kSyncTileRows tokens), and the row count addressed in int
+  if (a.T > ((int64_t)1 << 30)) return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  return true;
+}
+
+hipError_t launch_fused_large(const FwdArgs& a, hipStream_t st) {
+  FwdArgs b = a;
+  b.epoch = next_epoch();
+  hipLaunchKernelGGL((dev::k_fused_large<256, 1>), dim3(dev::fused::kGrid), dim3(256), 0, st, b,
+                     static_cast<const uint16_t*>(a.wfrag), static_cast<const uint16_t*>(a.cz),
+                     static_cast<const uint16_t*>(a.uoutT), static_cast<uint16_t*>(a.out),
+                     a.bias);
+  return hipGetLastError();
+}
+
+bool front_fuses_cz(const FwdArgs& a, hipStream_t st) {
   // launch_front_nr: k_front_part + k_front_epi when front_split > 1 (the per-token
   // epilogue writes c (x) z for any r1), else k_front_split for r3 = 256 with
   // E_pad = 256 (z and router in separate work-groups: no), else k_front (front_tile:
@@ -489,7 +520,15 @@ bool front_fuses_cz(const FwdArgs& a) {
   if (a.front_split > 1) return true;
   // k_front_split (r3 = 256, E_pad = 256): the z work-groups wait for the router
   // work-groups' c through the workspace's sync words
-  if (a.r3 == 256 && a.E_pad == 256) return a.r1 <= 32 && a.sync != nullptr;
+  // (not under graph capture: a consumer that gave up on its flag would leave it
+  // to be found set on a replay with the same epoch; the captured forward runs
+  // k_expand_cz instead)
+  if (a.r3 == 256 && a.E_pad == 256) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return false;
+    return a.r1 <= 32 && a.sync != nullptr;
+  }
   return a.r1 <= 32;
 }
 

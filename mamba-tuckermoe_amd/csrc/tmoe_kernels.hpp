@@ -847,20 +847,35 @@ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 // invalidate the whole L2 of an XCD, under the work-groups still computing there
 // (measured: the E_pad = 256 front at T = 4096 went from 35 to 72 us with an
 // acquire in the wait loop). sync_publish waits for the work-group's stores to
-// complete before the flag is written.
-// Consumers have higher work-group indices than their producers (work-groups
-// start in index order, so a waiting consumer never keeps its producer from
-// starting), wait at most kSyncLimitTicks of the 100 MHz real-time clock (past
-// it, sync[0] records the epoch and the consumer goes on with NaN in place of the
-// data), and, when a flag has one consumer, that consumer sets it back to 0 once
-// seen, so that a graph replay of the same launch (same epoch) waits again.
-constexpr uint64_t kSyncLimitTicks = 2000000;   // 20 ms
+// complete before the flag is written. (The one-launch large-T forward hands its
+// c (x) z rows over inside one XCD's L2 with plain stores and loads instead:
+// producer and consumers run on the same XCD, see tmoe_fused.hpp.)
+// Consumers have higher work-group indices than their producers, or all
+// work-groups of the launch are resident at once (one per compute unit), so a
+// waiting consumer never keeps its producer from running. A wait is bounded by a
+// number of polls of its flags (FwdArgs::wait_polls, set by the host; a poll
+// costs a device-scope load round trip and ~128 clocks of sleep). Past it the
+// epoch goes into sync[0], word kStatusSignal of the launch's host-visible status
+// block (FwdArgs::status) is set, and the consumer goes on with NaN in place of
+// the data, so that a lost signal surfaces as an error the host can read and as
+// NaN output, never as a hang. A budget of 0 gives up without polling (the host's
+// way to exercise this path with every kernel still exiting normally). When a
+// flag has one consumer, that consumer sets it back to 0 once seen (a second
+// launch with the same epoch, as a graph replay, then waits again); launches
+// whose flags have several consumers, or whose consumer may give up, are kept
+// out of graph capture by the launcher.
+constexpr int kStatusSignal = kStatusSignalWord;
 
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sets word `which` of the host-visible status block (no-op without one).
+__device__ __forceinline__ void report_status(uint32_t* status, int which) {
+  if (status) __hip_atomic_store(status + which, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __device__ __forceinline__ void sync_publish(uint32_t* flag, uint32_t epoch) {
@@ -871,34 +886,37 @@ __device__ __forceinline__ void sync_publish(uint32_t* flag, uint32_t epoch) {
 }
 
 // Called by every thread: waits for the n flags flags[0], flags[kSyncStride], ...;
-// true once all were seen, false when the wait ran out of time. The first wave
-// polls: lane l watches flags l, l + 64, ..., so that flags set at about the same
-// time cost one round trip, not one each. reset: the caller is the flags' only
-// consumer and sets them back to 0 (a flag several work-groups wait for stays
-// set; such launches are not replayed from a graph). seen_all: one word of the
-// kernel's LDS array for the answer (a __shared__ variable of its own changed how
-// the compiler tracks the kernel's LDS DMA: it then waited for every DMA before
-// each fragment read of the main loop). The work-group has at least 64 threads.
+// true once all were seen, false when the wait ran out of its budget of `polls`
+// polls (see above; the error is then recorded in *err and the status block).
+// The first wave polls: lane l watches flags l, l + 64, ..., so that flags set at
+// about the same time cost one round trip, not one each. reset: the caller is the
+// flags' only consumer and sets them back to 0 once seen. seen_all: one word of
+// the kernel's LDS array for the answer (a __shared__ variable of its own changed
+// how the compiler tracks the kernel's LDS DMA: it then waited for every DMA
+// before each fragment read of the main loop). The work-group has at least 64
+// threads.
 __device__ __forceinline__ bool sync_await(uint32_t* flags, int n, uint32_t epoch, uint32_t* err,
-                                           int* seen_all, bool reset) {
+                                           int* seen_all, bool reset, int polls,
+                                           uint32_t* status) {
   if (threadIdx.x < 64) {   // the whole first wave
     const int l = threadIdx.x;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     int next = l;   // the lane's first flag not yet seen
-    bool seen = true;
-    while (true) {
+    bool seen = n <= 0;
+    for (int p = 0; p < polls && !seen; ++p) {
       while (next < n && __hip_atomic_load(flags + (int64_t)next * kSyncStride, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT) == epoch)
         next += 64;
-      if (__all(next >= n)) break;
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncLimitTicks) {
-        seen = false;
+      if (__all(next >= n)) {
+        seen = true;
         break;
       }
       __builtin_amdgcn_s_sleep(2);   // ~128 clocks between polls
     }
     if (!seen) {
-      if (l == 0) __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (l == 0) {
+        __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        report_status(status, kStatusSignal);
+      }
     } else if (reset) {
       for (int i = l; i < n; i += 64)
         __hip_atomic_store(flags + (int64_t)i * kSyncStride, 0u, __ATOMIC_RELAXED,
@@ -1519,7 +1537,8 @@ __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
         // RMSNorm partials; NaN when the wait ran out of time
         float* cl = reinterpret_cast<float*>(zst + kZEpi);
         const bool ok = sync_await(a.sync + sync_flag(tm), 1, a.epoch, a.sync,
-                                   reinterpret_cast<int*>(cl + BM * 32), true);
+                                   reinterpret_cast<int*>(cl + BM * 32), true, a.wait_polls,
+                                   a.status);
         const int n = rows_valid * (int)a.r1;
         for (int q = threadIdx.x; q < n; q += TLZ::kThreads)
           cl[q] = ok ? load_coherent(a.c + m0 * a.r1 + q) : __builtin_nanf("");

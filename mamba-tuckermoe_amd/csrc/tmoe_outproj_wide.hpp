@@ -91,15 +91,17 @@ __device__ __forceinline__ void wide_step(f32x16 (&acc)[FM][wide::FN], const u32
   for (int m = FM * wide::FN; m < FM + wide::FN; ++m) ld(m);
 }
 
-// A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32. The pointers
-// are separate restrict parameters: that lets the compiler read bias through
-// the scalar unit (it may assume no store of C clobbers it).
-template <int FM_>
-__global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict__ A,
-                                                      const uint16_t* __restrict__ Bt,
-                                                      uint16_t* __restrict__ C,
-                                                      const float* __restrict__ bias, int M,
-                                                      int N, int K) {
+// The tile loop of a work-group: out = A Bt^T + bias over the tiles a schedule
+// hands it. Sched: start(tm, tn) gives the first tile (false: none) and
+// advance(tm, tn) the next (false: no more), both called uniformly by the whole
+// work-group. A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32.
+// smem: 2 Cfg<FM>::kStage 16-byte slots of LDS.
+template <int FM_, class Sched>
+__device__ __forceinline__ void wide_loop(const uint16_t* __restrict__ A,
+                                          const uint16_t* __restrict__ Bt,
+                                          uint16_t* __restrict__ C,
+                                          const float* __restrict__ bias, int M, int N, int K,
+                                          u32x4* smem, Sched& sched) {
   using wide::FN;
   using wide::BN;
   using wide::kAgprBlk;
@@ -107,21 +109,16 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
   constexpr int FM = Cf::FM, BM = Cf::BM, kStage = Cf::kStage;
   constexpr int kDmaPerWave = Cf::kDmaPerWave, kABlocksPerWave = Cf::kABlocksPerWave;
   constexpr int kStores = Cf::kStores;
-  __shared__ u32x4 smem[2 * kStage];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ntn = N / BN;
-  const int ntiles = ((M + BM - 1) / BM) * ntn;
   const int nkt = K / 64;
   const uint32_t row_bytes = (uint32_t)K * 2;
 
   f32x16 acc[FM][FN];
   u32x4 fa[2][FM], fb[2][FN];
 
-  int t = blockIdx.x;
-  if (t >= ntiles) return;
   int tm, tn;
-  tile_coords_of(t, ntn, ntiles, tm, tn);
+  if (!sched.start(tm, tn)) return;
 
   // DMA block wave + 4 d of a stage: A rows 32 d + 8 wave + (lane >> 3) for
   // d < kABlocksPerWave, else W^T rows 32 (d - kABlocksPerWave) + 8 wave +
@@ -210,12 +207,10 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
     if (nkt > 1) ktile(nkt - 1, false, false, true, false);
     // the next tile's first two K tiles into stages 0 and 1 (both free: every
     // read of them completed before the last barrier), ahead of the stores
-    const int t_next = t + (int)gridDim.x;
-    const bool has_next = t_next < ntiles;
-    const bool early = has_next && nkt > 1;
     int tm2 = tm, tn2 = tn;
+    const bool has_next = sched.advance(tm2, tn2);
+    const bool early = has_next && nkt > 1;
     if (has_next) {
-      tile_coords_of(t_next, ntn, ntiles, tm2, tn2);
 #pragma unroll
       for (int d = 0; d < kDmaPerWave; ++d) dma(d, 0, 0, tm2, tn2);
       if (early) {
@@ -281,7 +276,6 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
       }
     }
     if (!has_next) break;
-    t = t_next;
     tm = tm2;
     tn = tn2;
     // K tile 0 has landed once at most the DMAs of K tile 1 and the stores remain
@@ -294,6 +288,39 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
     pre = early;
     pre_full = full;
   }
+}
+
+
+// Work-group b's tiles: b, b + grid, ... of the (M / BM) x (N / BN) tile grid, in
+// tile_coords_of's XCD-aware order.
+struct WideGridSched {
+  int t, ntn, ntiles;
+  __device__ __forceinline__ bool start(int& tm, int& tn) {
+    t = blockIdx.x;
+    if (t >= ntiles) return false;
+    tile_coords_of(t, ntn, ntiles, tm, tn);
+    return true;
+  }
+  __device__ __forceinline__ bool advance(int& tm, int& tn) {
+    t += (int)gridDim.x;
+    if (t >= ntiles) return false;
+    tile_coords_of(t, ntn, ntiles, tm, tn);
+    return true;
+  }
+};
+
+// The pointers are separate restrict parameters: that lets the compiler read bias
+// through the scalar unit (it may assume no store of C clobbers it).
+template <int FM_>
+__global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict__ A,
+                                                      const uint16_t* __restrict__ Bt,
+                                                      uint16_t* __restrict__ C,
+                                                      const float* __restrict__ bias, int M,
+                                                      int N, int K) {
+  typedef wide::Cfg<FM_> Cf;
+  __shared__ u32x4 smem[2 * Cf::kStage];
+  WideGridSched sched{0, N / wide::BN, ((M + Cf::BM - 1) / Cf::BM) * (N / wide::BN)};
+  wide_loop<FM_>(A, Bt, C, bias, M, N, K, smem, sched);
 }
 
 #undef TMOE_MFMA_A

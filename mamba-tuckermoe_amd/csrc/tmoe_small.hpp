@@ -723,7 +723,7 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
     for (int q = 0; q < 4; ++q) gv[j][q] = g < NG ? a.gain[col + q] : 0.f;
   }
   const bool ok = sync_await(a.sync + sync_flag(0), NP, a.epoch, a.sync,
-                             reinterpret_cast<int*>(red), false);
+                             reinterpret_cast<int*>(red), false, a.wait_polls, a.status);
   // every load first: the z groups and c
   const __amdgpu_buffer_rsrc_t rz = coherent_rsrc(sc.zr, (int64_t)Tn * R3);
   f32x4 zv[kDecodeGroups];

@@ -22,16 +22,31 @@ void* g_ptr[kMaxDevices];   // device address of `scratch` on each GPU (null: no
 
 namespace tmoe {
 
-hipError_t static_scratch(void** ptr) {
+hipError_t static_scratch(hipStream_t stream, void** ptr) {
   *ptr = nullptr;
-  int dev = -1;
-  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  int cur = -1;
+  if (hipError_t e = hipGetDevice(&cur); e != hipSuccess) return e;
+  // the device the forward's kernels run on: the stream's (the null stream: the
+  // current device's)
+  int dev = cur;
+  if (stream) {
+    hipDevice_t d = -1;
+    if (hipError_t e = hipStreamGetDevice(stream, &d); e != hipSuccess) return e;
+    dev = (int)d;
+  }
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(g_mu);
   if (!g_ptr[dev]) {
+    // with `dev` current: the address of that GPU's copy
+    if (dev != cur)
+      if (hipError_t e = hipSetDevice(dev); e != hipSuccess) return e;
     void* p = nullptr;
-    // with `dev` current: the address of this GPU's copy
-    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return e;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
     g_ptr[dev] = p;
   }

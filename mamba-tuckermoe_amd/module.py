@@ -41,32 +41,49 @@ from . import fp8 as _fp8
 
 
 class TrackedParameter(nn.Parameter):
-    """nn.Parameter that counts accesses to `.data`.
+    """nn.Parameter whose in-place writes through `.data` are seen.
 
     In-place writes through `param.data` (the reference loader,
     pure_torch_mlx/weights.py:74-81: `moe.U_in.data.copy_(w[...])`) bypass the
     parameter's version counter, which is what a cache of derived state usually
-    keys on. Every get or set of `.data` increments `tracked_gen(param)`, which
-    TuckerMoE's packed-weight cache key includes. Behaves as nn.Parameter
-    otherwise (state_dict, load_state_dict, .to(), deepcopy keep the class)."""
+    keys on: `.data` returns an alias with a version counter of its own. Here the
+    getter hands out one alias per parameter storage (kept until the parameter's
+    data changes), so writes through it move that alias's counter, which
+    `tracked_gen(param)` reports along with the count of `.data` assignments;
+    TuckerMoE's packed-weight cache key includes it. Reading `.data` changes
+    nothing, so it costs no re-pack. Behaves as nn.Parameter otherwise
+    (state_dict, load_state_dict, .to(), deepcopy keep the class)."""
 
     def __new__(cls, data=None, requires_grad=True):
         return super().__new__(cls, data, requires_grad)
 
     @property
     def data(self):
-        self.__dict__["_tmoe_gen"] = self.__dict__.get("_tmoe_gen", 0) + 1
-        return torch.Tensor.data.__get__(self)
+        d = self.__dict__
+        cur = torch.Tensor.data.__get__(self)
+        al = d.get("_tmoe_alias")
+        if (al is None or al.data_ptr() != cur.data_ptr() or al.shape != cur.shape
+                or al.stride() != cur.stride() or al.dtype != cur.dtype
+                or al.device != cur.device):
+            # a new alias (first access, or the parameter's data changed): its
+            # counter starts anew, so the generation moves
+            d["_tmoe_alias"] = cur
+            d["_tmoe_gen"] = d.get("_tmoe_gen", 0) + 1
+            return cur
+        return al
 
     @data.setter
     def data(self, value):
         self.__dict__["_tmoe_gen"] = self.__dict__.get("_tmoe_gen", 0) + 1
+        self.__dict__.pop("_tmoe_alias", None)
         torch.Tensor.data.__set__(self, value)
 
 
-def tracked_gen(p: torch.Tensor) -> int:
-    """Number of `.data` accesses of a TrackedParameter (0 for other tensors)."""
-    return p.__dict__.get("_tmoe_gen", 0)
+def tracked_gen(p: torch.Tensor):
+    """(assignments of `.data`, writes through the alias `.data` returns) of a
+    TrackedParameter; (0, 0) for other tensors."""
+    al = p.__dict__.get("_tmoe_alias")
+    return (p.__dict__.get("_tmoe_gen", 0), al._version if al is not None else 0)
 
 
 def _tracked(p: nn.Parameter) -> TrackedParameter:
@@ -172,13 +189,40 @@ class TuckerMoE(nn.Module):
         takes fewer multiply-adds per token; ``set_fold(False)`` keeps the core
         contraction (model.py:87-98) and the out-projection (model.py:101) as two
         GEMMs. Takes effect at the next forward (the weights are re-packed)."""
-        flags = 0 if enabled else _lib.TMOE_FLAG_NO_FOLD
+        flags = (self._plan_flags & ~_lib.TMOE_FLAG_NO_FOLD) | (
+            0 if enabled else _lib.TMOE_FLAG_NO_FOLD)
         if flags != self._plan_flags:
             self._plan_flags = flags
             self._plan = None
             self._packed = None
             self._packed_key = None
         return self
+
+    def set_fuse(self, enabled: bool = True) -> "TuckerMoE":
+        """Whether the library may run a large-T forward as one launch (default): the
+        front and the out-projection in one persistent grid that hands c (x) z over
+        inside each XCD (folded bf16 plans with r3 = 256, E <= 32, d_out a multiple
+        of 288, T >= 8192 at d_out = 2304). ``set_fuse(False)`` keeps two launches.
+        The packed weights are the same either way."""
+        flags = (self._plan_flags & ~_lib.TMOE_FLAG_NO_FUSE) | (
+            0 if enabled else _lib.TMOE_FLAG_NO_FUSE)
+        if flags != self._plan_flags:
+            self._plan_flags = flags
+            self._plan = None
+        return self
+
+    def check_signals(self) -> None:
+        """Synchronises the parameters' device and raises RuntimeError (a
+        _lib.TmoeError with code TMOE_ESIGNAL) if a forward of this module since the
+        last check lost an in-launch signal: a kernel whose work-groups hand data to
+        each other gave up waiting (the affected output rows are NaN or stale).
+        forward() runs the same check without synchronising, for the forwards that
+        have completed."""
+        if self._plan is None:
+            return
+        if self.U_in.device.type == "cuda":
+            torch.cuda.synchronize(self.U_in.device)
+        self._plan.signal_status(clear=True)
 
     # -- router mode -------------------------------------------------------------
     def set_router_mode(self, mode: str = "softmax_topk", scale: float = 10.0,
@@ -352,6 +396,9 @@ class TuckerMoE(nn.Module):
         d_out = self.U_out.shape[1]
         E = self.U_expert.shape[0]
         plan = self.plan()
+        # an earlier forward's kernel that lost an in-launch signal (host memory the
+        # kernels write: no synchronisation) is reported before any new work
+        plan.signal_status(clear=True)
         packed = self.packed()
         dev = X.device
         if out is None:

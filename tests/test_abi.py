@@ -56,7 +56,7 @@ def _create(pkg, **kw):
     (dict(E=32, k=17), -2, "top_k=17"),
     (dict(r1=65), -2, "r1"),
     (dict(router_mode=2), -1, "router_mode"),
-    (dict(flags=2), -1, "flags"),
+    (dict(flags=4), -1, "flags"),
     (dict(router_mode=1, router_scale=0.0, router_temperature=0.5), -1, "router_scale"),
     (dict(router_mode=1, router_scale=10.0, router_temperature=-1.0), -1, "router_temperature"),
 ])
@@ -300,3 +300,46 @@ def test_forward_static_rejects_before_gpu_work(pkg):
         assert L.tmoe_forward_static(p, 8, 64, 16, 16, None, None, None, None) == -1  # misaligned
     finally:
         L.tmoe_plan_destroy(p)
+
+
+def test_signal_status_host_side(pkg):
+    """tmoe_signal_status reads the plan's status block on the host: a null plan is
+    EINVAL; a fresh plan reports nothing (on a machine without a GPU the block is
+    never allocated and nothing can have run). tmoe_set_wait_polls returns the
+    previous budget and ignores a negative one."""
+    L = pkg._lib.lib()
+    mask = ctypes.c_uint32(7)
+    assert L.tmoe_signal_status(None, 0, ctypes.byref(mask)) == pkg._lib.TMOE_EINVAL
+    assert mask.value == 0 and "null plan" in L.tmoe_last_error().decode()
+    rc, p, _ = _create(pkg)
+    assert rc == 0
+    try:
+        assert L.tmoe_signal_status(p, 1, ctypes.byref(mask)) == pkg._lib.TMOE_OK
+        assert mask.value == 0
+        assert L.tmoe_signal_status(p, 0, None) == pkg._lib.TMOE_OK
+    finally:
+        L.tmoe_plan_destroy(p)
+    plan = pkg._lib.Plan(512, 1024, 8, 2, 4, 256, 128, torch.float32, 1e-5)
+    assert plan.signal_status() == 0
+    prev = pkg._lib.set_wait_polls(-1)
+    assert prev >= 0
+    try:
+        assert pkg._lib.set_wait_polls(5) == prev
+        assert pkg._lib.set_wait_polls(-3) == 5
+    finally:
+        pkg._lib.set_wait_polls(prev)
+    assert pkg._lib.set_wait_polls(-1) == prev
+
+
+@pytest.mark.parametrize("flags,ok", [(0, True), (1, True), (2, True), (3, True), (4, False),
+                                      (8, False)])
+def test_plan_flags(pkg, flags, ok):
+    """TMOE_FLAG_NO_FOLD (1) and TMOE_FLAG_NO_FUSE (2) are the only plan flags."""
+    rc, p, err = _create(pkg, flags=flags)
+    try:
+        assert (rc == 0) == ok, err
+        if not ok:
+            assert rc == pkg._lib.TMOE_EINVAL and "flags" in err
+    finally:
+        if p.value:
+            pkg._lib.lib().tmoe_plan_destroy(p)

@@ -151,6 +151,27 @@ def test_data_writes_invalidate_packed_key(pkg):
     assert m._packed is None               # load_state_dict forgets the packed copy
 
 
+def test_data_reads_keep_packed_key(pkg):
+    """Reading a weight through `.data` (inspection, norms, copies out) writes
+    nothing, so it must not force a re-pack (at C3 a re-fold of W costs ~0.2 ms);
+    a write through the same alias still does, as does assigning `.data`."""
+    w = pkg.WORKLOADS["C1"]
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg())
+    m.load_state_dict(pkg.synth.make_params(w))
+    for p in m._params():
+        _ = p.data                         # the first access hands out the alias
+        k0 = m._key()
+        for _ in range(3):
+            float(p.data.float().abs().sum())
+            _ = p.data.clone()
+        assert m._key() == k0
+        p.data.mul_(1.0)                   # an in-place write through .data
+        k1 = m._key()
+        assert k1 != k0
+        p.data = p.detach().clone()        # assignment
+        assert m._key() != k1
+
+
 def test_tracked_parameters_survive_conversion(pkg):
     import copy
     w = pkg.WORKLOADS["C1"]
