@@ -313,6 +313,8 @@ def main():
                     help="time the FFN sub-block of this FFN workload (F0, F1, F2) instead")
     ap.add_argument("--no-fold", action="store_true",
                     help="keep the core and the out-projection as two GEMMs (TMOE_FLAG_NO_FOLD)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the extra workloads (C2, C4, C3 at T=2048 and T=1) of the C3 run")
     ap.add_argument("--no-fuse", action="store_true",
                     help="never run the large-T forward as one launch (TMOE_FLAG_NO_FUSE)")
     ap.add_argument("--latent", action="store_true",
@@ -331,16 +333,52 @@ def main():
         bench_latent(args)
         return
 
-    import numpy as np
     import torch
 
     import __graft_entry__
     pkg = __graft_entry__.load_package()
-    L = pkg._lib.lib()
-
     w = pkg.WORKLOADS[args.workload]
     if args.tokens:
         w = w.with_T(args.tokens)
+    r = measure(pkg, w, args, steps=args.steps, warmup=args.warmup, rotate_mb=args.rotate_mb,
+                no_fold=args.no_fold, no_fuse=args.no_fuse, cpu=not args.no_cpu, label="bench")
+    res = r["result"]
+    # the other workloads' figures, measured in the same run (their own parity slices;
+    # the headline above is unchanged by them)
+    if not args.no_extra and args.workload == "C3" and not args.tokens:
+        extra = {}
+        for key, name, T in EXTRA_WORKLOADS:
+            we = pkg.WORKLOADS[name].with_T(T) if T else pkg.WORKLOADS[name]
+            e = measure(pkg, we, args, steps=args.steps, warmup=args.warmup,
+                        rotate_mb=args.rotate_mb, no_fold=args.no_fold, no_fuse=args.no_fuse,
+                        cpu=False, label=f"extra {key}")
+            rr = e["result"]
+            extra[key] = {
+                "workload": rr["config"]["workload"], "T": rr["config"]["T"],
+                "ms_per_step": rr["ms_per_step"], "avg_us": rr["ms_per_step"] * 1e3,
+                "tokens_per_s": rr["value"], "path": rr["config"]["path"],
+                "roofline": {k: rr["roofline"][k] for k in
+                             ("bound", "kernel", "achieved", "peak", "unit", "frac", "avg_us")},
+                "layer": {k: rr["layer"][k] for k in
+                          ("executed_tflops", "executed_mfma_frac", "tflops", "mfma_frac",
+                           "hbm_gbs_compulsory")},
+                "parity": rr["parity"],
+            }
+        res["extra"] = extra
+    print(json.dumps(res), flush=True)
+
+
+# the workloads measured beside the C3 headline: (key, workload, T or None)
+EXTRA_WORKLOADS = (("C2", "C2", None), ("C4", "C4", None),
+                   ("C3_T2048", "C3", 2048), ("C3_T1", "C3", 1))
+
+
+def measure(pkg, w, args, *, steps, warmup, rotate_mb, no_fold, no_fuse, cpu, label):
+    """One workload: warm-up, `steps` timed forwards over rotated buffer sets, the
+    per-stage event pass, parity on a slice and (cpu) the host baseline. Returns
+    {"result": the JSON fields of the bench line}."""
+    import torch
+    L = pkg._lib.lib()
     T = w.T
     dev = torch.device("cuda:0")
     dt_name = "bf16" if w.dtype == torch.bfloat16 else "f32"
@@ -363,8 +401,8 @@ def main():
     x0 = pkg.synth.make_x(w)
     m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(dev, w.dtype)
     m.load_state_dict({k: v.to(dev) for k, v in params.items()})
-    m.set_fold(not args.no_fold)
-    m.set_fuse(not args.no_fuse)
+    m.set_fold(not no_fold)
+    m.set_fuse(not no_fuse)
     if codes is not None:
         m.load_fp8(*[codes[k].to(dev) for k in ("U_in_q", "U_in_scale", "core_q", "core_scale",
                                                   "U_out_q", "U_out_scale")])
@@ -372,13 +410,14 @@ def main():
     packed0 = m.packed()
     folded = plan.folded()
     rk = plan.core_rank()
+    path = plan.forward_path(T)
     form = ("folded: c (x) z against W = core U_out, one GEMM of width %d" % (rk * w.r3)
             if folded else "two GEMMs: core (rank %d) then U_out" % rk)
-    log(f"[bench] plan form: {form}")
+    log(f"[{label}] plan form: {form}; kernels: {pkg._lib.PATH_NAMES.get(path, path)}")
     ws_bytes = plan.workspace_bytes(T)
     set_bytes = T * w.d_in * es + T * w.d_out * es + ws_bytes + packed0.numel()
-    n_sets = max(3, math.ceil(args.rotate_mb * 1e6 / set_bytes))
-    log(f"[bench] workload {w.name}: T={T} d_in={w.d_in} d_out={w.d_out} E={w.E} k={w.k} "
+    n_sets = max(3, math.ceil(rotate_mb * 1e6 / set_bytes))
+    log(f"[{label}] workload {w.name}: T={T} d_in={w.d_in} d_out={w.d_out} E={w.E} k={w.k} "
         f"r=({w.r1},{w.r3},{w.r2}) {dt_name}; {n_sets} rotated sets x {set_bytes / 1e6:.1f} MB")
     gen = torch.Generator(device=dev).manual_seed(w.seed)
     sets = []
@@ -400,28 +439,29 @@ def main():
             pkg._lib.check(rc)
 
     # -- warmup + timed region ------------------------------------------------
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = ev0.elapsed_time(ev1)
-    ms_per_step = gpu_ms / args.steps
-    tok_s = T * args.steps / (gpu_ms / 1e3)
-    log(f"[bench] {args.steps} steps: {gpu_ms:.3f} ms on the stream ({wall * 1e3:.3f} ms wall), "
+    ms_per_step = gpu_ms / steps
+    tok_s = T * steps / (gpu_ms / 1e3)
+    log(f"[{label}] {steps} steps: {gpu_ms:.3f} ms on the stream ({wall * 1e3:.3f} ms wall), "
         f"{ms_per_step * 1e3:.2f} us/step, {tok_s / 1e6:.2f} M tok/s")
+    plan.signal_status()   # raises if a kernel lost an in-launch signal
 
     # -- per-stage kernel durations (HIP events recorded by the library) ---------
     pkg._lib.prof_enable(True)
     try:
-        for i in range(args.steps):
+        for i in range(steps):
             step(i)
         torch.cuda.synchronize()
         stage_ms, calls = pkg._lib.prof_read()
@@ -432,15 +472,17 @@ def main():
     fl = w.flops_executed(T, rk, folded)        # the dominant kernel's own work
     fl["front"] = fl["router"] + fl["in_proj"]   # one kernel computes both
     sb = w.stage_bytes_folded(T, rk) if folded else w.stage_bytes()
-    one_launch = w.one_launch(T, rk, folded)
+    one_launch = path in (pkg._lib.TMOE_PATH_DECODE, pkg._lib.TMOE_PATH_FUSED)
+    kname = {pkg._lib.TMOE_PATH_DECODE: "k_sk_decode", pkg._lib.TMOE_PATH_FUSED: "k_fused_large"}
     if one_launch:
-        # the decode kernel (recorded as the front stage) runs the whole layer; the
-        # other two stages record no kernel
+        # the one kernel (recorded as the front stage) runs the whole layer; the other
+        # two stages record no kernel
         fl["front"] = fl["total"]
         sb["front"] = w.layer_bytes_folded(T, rk)
-        log("[bench] one launch (k_sk_decode): the front stage is the whole layer")
+        log(f"[{label}] one launch ({kname[path]}): the front stage is the whole layer")
     dom = max(stage_avg_us, key=stage_avg_us.get)
-    dom_label = "front = whole layer (k_sk_decode, one launch)" if one_launch and dom == "front" else dom
+    dom_label = (f"front = whole layer ({kname[path]}, one launch)"
+                 if one_launch and dom == "front" else dom)
     dom_tflops = fl[dom] / (stage_avg_us[dom] * 1e-6) / 1e12
     dom_gbs = sb[dom] / (stage_avg_us[dom] * 1e-6) / 1e9
     peak = PEAK_TFLOPS[dt_name]
@@ -449,27 +491,28 @@ def main():
     mfma_bound = fl[dom] / sb[dom] >= peak * 1e12 / (HBM_PEAK_GBS * 1e9)
     layer_tflops = fl_algo["total"] / (ms_per_step * 1e-3) / 1e12
     layer_exec_tflops = fl["total"] / (ms_per_step * 1e-3) / 1e12
-    log("[bench] per-stage avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in stage_avg_us.items()))
-    log(f"[bench] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak, "
+    log(f"[{label}] per-stage avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in stage_avg_us.items()))
+    log(f"[{label}] dominant kernel {dom}: {dom_tflops:.1f} TFLOP/s = {dom_tflops / peak:.3f} of peak, "
         f"{dom_gbs:.1f} GB/s = {dom_gbs / HBM_PEAK_GBS:.3f} of HBM; "
         f"layer {layer_exec_tflops:.1f} TFLOP/s executed = {layer_exec_tflops / peak:.3f} of peak; "
         f"{layer_tflops:.1f} TFLOP/s = {layer_tflops / peak:.3f} counting the reference form's flops")
 
-    if args.copy_calibration_mib:
+    if getattr(args, "copy_calibration_mib", 0) and label == "bench":
         n = args.copy_calibration_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        log(f"[bench] copy calibration: 3 x {args.copy_calibration_mib} MiB device copies")
+        log(f"[{label}] copy calibration: 3 x {args.copy_calibration_mib} MiB device copies")
 
     full_size = T == pkg.WORKLOADS[w.name].T
-    traffic = (traffic_per_launch(w.name, dom + ("_folded" if folded else ""))
-               if full_size else None)
+    stage_key = dom + ("_fused" if path == pkg._lib.TMOE_PATH_FUSED else
+                       "_folded" if folded else "")
+    traffic = traffic_per_launch(w.name, stage_key) if full_size else None
     # MFMA-busy share of the dominant stage from the committed counter pass (the
     # timing-derived share is `frac`: executed flops / avg duration / peak at 2.4 GHz)
-    mfma_util = (profile_figure(w.name, "mfma_util", dom + "_folded")
+    mfma_util = (profile_figure(w.name, "mfma_util", stage_key)
                  if full_size and folded else None)
 
     # -- parity on a slice (GPU result of set 0 vs the fp32 reference path) --------
@@ -491,25 +534,25 @@ def main():
         "reference": "oracle/tucker_moe_torch fp32 on the bf16-valued inputs"
                      + (" and the dequantised e4m3 weights" if w.fp8 else ""),
     }
-    log(f"[bench] parity on {n_par} tokens: {parity}")
+    log(f"[{label}] parity on {n_par} tokens: {parity}")
 
     # -- host-CPU baseline (rank 0, N=1): the reference op sequence on the CPU --------
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(lambda xs, **kw: ot.forward(xs, params, w.k, **kw), x0, T, 512,
-                           args.cpu_seconds, f"{w.name}", dt_name,
-                           "reference op sequence (oracle/tucker_moe_torch)",
-                           oracle_mode=dt_name != "f32")
-        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads "
-            f"({cpu['tokens']} tokens, median of 3 passes {cpu['seconds']:.2f} s)")
+    cpu_res = None
+    if cpu:
+        cpu_res = cpu_baseline(lambda xs, **kw: ot.forward(xs, params, w.k, **kw), x0, T, 512,
+                               args.cpu_seconds, f"{w.name}", dt_name,
+                               "reference op sequence (oracle/tucker_moe_torch)",
+                               oracle_mode=dt_name != "f32")
+        log(f"[{label}] CPU baseline: {cpu_res['value']:.1f} tok/s on {cpu_res['cores']} threads "
+            f"({cpu_res['tokens']} tokens, median of 3 passes {cpu_res['seconds']:.2f} s)")
 
     res = {
         "metric": METRIC,
         "value": tok_s,
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -525,7 +568,7 @@ def main():
                                if w.fp8 and folded else
                                "U_in/core/U_out fp8 e4m3 + per-output-channel fp32 scales, "
                                "unpacked exactly to bf16; bf16 MFMA" if w.fp8 else dt_name),
-                   "form": form},
+                   "form": form, "path": pkg._lib.PATH_NAMES.get(path, str(path))},
         "roofline": ({"bound": "mfma", "kernel": dom_label, "achieved": dom_tflops, "peak": peak,
                       "unit": "TFLOP/s", "frac": dom_tflops / peak, "traffic": traffic,
                       "mfma_util_counter": mfma_util,
@@ -547,10 +590,12 @@ def main():
                   "hbm_gbs_compulsory": w.hbm_bytes() / (ms_per_step * 1e-3) / 1e9,
                   "stage_avg_us": stage_avg_us},
         "parity": parity,
-        "cpu_baseline": cpu,
-        "speedup_vs_cpu": (tok_s / cpu["value"]) if cpu else None,
+        "cpu_baseline": cpu_res,
+        "speedup_vs_cpu": (tok_s / cpu_res["value"]) if cpu_res else None,
     }
-    print(json.dumps(res), flush=True)
+    del sets
+    torch.cuda.empty_cache()
+    return {"result": res}
 
 
 if __name__ == "__main__":

@@ -245,6 +245,16 @@ int tmoe_forward_static(const tmoe_plan* plan, const void* x, int64_t T, const v
                         void* out, int32_t* topk_idx, float* topk_w, float* logits,
                         void* stream);
 
+/* The kernel sequence an eager tmoe_forward of T tokens runs with this plan on the
+ * current device (on a machine without a GPU: as on a 256-compute-unit MI355X).
+ * No counterpart in the reference; for measurement tools, which attribute time
+ * per kernel. Returns one of TMOE_PATH_* (0 for T == 0) or a negative error. */
+#define TMOE_PATH_SMALL  1  /* T <= 256: skinny kernels, two or three launches        */
+#define TMOE_PATH_DECODE 2  /* T <= 64, bf16, folded: the whole layer in one launch   */
+#define TMOE_PATH_LARGE  3  /* front, (core or c (x) z), out-projection launches      */
+#define TMOE_PATH_FUSED  4  /* large T, folded: the whole layer in one launch         */
+int tmoe_forward_path(const tmoe_plan* plan, int64_t T);
+
 /* Lost in-launch signals. No counterpart in the reference (its forward has no
  * kernels that wait for each other; torch raises its errors from the call).
  * A kernel whose wait for another work-group of its launch runs out of its poll

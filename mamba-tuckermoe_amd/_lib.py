@@ -27,6 +27,9 @@ TMOE_EPI_NONE, TMOE_EPI_GLU, TMOE_EPI_RESIDUAL_SCALE = 0, 1, 2
 TMOE_FLAG_NO_FOLD = 1
 TMOE_FLAG_NO_FUSE = 2
 TMOE_STATUS_SIGNAL = 1
+TMOE_PATH_SMALL, TMOE_PATH_DECODE, TMOE_PATH_LARGE, TMOE_PATH_FUSED = 1, 2, 3, 4
+PATH_NAMES = {1: "small-T kernels", 2: "one launch (k_sk_decode)",
+              3: "front + out-projection launches", 4: "one launch (k_fused_large)"}
 TMOE_LATENT_P_F32 = 0x100   # or'ed into a latent call's dtype: p and dp are fp32
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")
@@ -40,7 +43,7 @@ EXPORTED = (
     "tmoe_forward", "tmoe_forward_epi", "tmoe_forward_glu", "tmoe_rmsnorm_rows",
     "tmoe_static_scratch_bytes", "tmoe_forward_static",
     "tmoe_latent_workspace_bytes", "tmoe_latent_forward", "tmoe_latent_backward",
-    "tmoe_signal_status", "tmoe_set_wait_polls",
+    "tmoe_signal_status", "tmoe_set_wait_polls", "tmoe_forward_path",
     "tmoe_prof_enable", "tmoe_prof_read",
 )
 
@@ -129,6 +132,8 @@ def lib() -> ctypes.CDLL:
                                            ctypes.c_int, vp, vp, vp, vp, sz, vp]
         L.tmoe_signal_status.restype = ctypes.c_int
         L.tmoe_signal_status.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint32)]
+        L.tmoe_forward_path.restype = ctypes.c_int
+        L.tmoe_forward_path.argtypes = [vp, i64]
         L.tmoe_set_wait_polls.restype = ctypes.c_int64
         L.tmoe_set_wait_polls.argtypes = [i64]
         L.tmoe_prof_enable.restype = ctypes.c_int
@@ -205,6 +210,10 @@ class Plan:
     def folded(self) -> bool:
         """True if the forward runs one GEMM of c (x) z against W = core U_out."""
         return bool(lib().tmoe_plan_folded(self._ptr))
+
+    def forward_path(self, T: int) -> int:
+        """TMOE_PATH_* of an eager forward of T tokens on the current device."""
+        return check(lib().tmoe_forward_path(self._ptr, int(T)))
 
     def signal_status(self, clear: bool = True) -> int:
         """The TMOE_STATUS_* bits that completed kernels of this plan's forwards set

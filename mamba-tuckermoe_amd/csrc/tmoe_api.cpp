@@ -807,6 +807,29 @@ int tmoe_latent_backward(const void* x, const void* G, const int64_t* idx, const
   return e == hipSuccess ? TMOE_OK : hip_fail(e, "tmoe_latent_backward");
 }
 
+int tmoe_forward_path(const tmoe_plan* p, int64_t T) {
+  g_err[0] = 0;
+  if (!p) return fail(TMOE_EINVAL, "tmoe_forward_path: null plan");
+  if (T < 0) return fail(TMOE_EINVAL, "tmoe_forward_path: T=%lld < 0", (long long)T);
+  if (T == 0) return 0;
+  // the arguments of an eager forward with stand-in addresses (nothing is launched
+  // or dereferenced: the selection rules look at shapes and at which buffers exist)
+  char* const fake = reinterpret_cast<char*>(uintptr_t(1) << 20);
+  const Layout L = workspace_layout(p, T);
+  tmoe::FwdArgs a = make_args(p, fake, T, fake, fake, nullptr, nullptr, nullptr, fake, L);
+  if (T <= tmoe::kSmallT) {
+    if (p->fold) {
+      tmoe::FwdArgs f = folded_args(p, a, fake, nullptr);
+      if (tmoe::small_decode_shape_ok(f)) return TMOE_PATH_DECODE;
+    }
+    return TMOE_PATH_SMALL;
+  }
+  if (p->fold && !(p->s.flags & TMOE_FLAG_NO_FUSE) &&
+      tmoe::fused_large_shape_ok(folded_args(p, a, fake, nullptr)))
+    return TMOE_PATH_FUSED;
+  return TMOE_PATH_LARGE;
+}
+
 int tmoe_signal_status(const tmoe_plan* plan, int clear, uint32_t* mask) {
   g_err[0] = 0;
   if (mask) *mask = 0;

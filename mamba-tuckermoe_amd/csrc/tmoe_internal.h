@@ -235,6 +235,9 @@ bool front_fuses_cz(const FwdArgs& a, hipStream_t stream);
 // compute unit, c (x) z handed over inside each XCD's L2. fused_large_ok: the plan,
 // T, the device and the stream allow it (f: the folded forward's arguments).
 bool fused_large_ok(const FwdArgs& f, hipStream_t stream);
+// the same rules without the stream's capture state (an eager forward)
+bool fused_large_shape_ok(const FwdArgs& f);
+bool small_decode_shape_ok(const FwdArgs& a);
 hipError_t launch_fused_large(const FwdArgs& f, hipStream_t stream);
 // small-T path: front = skinny GEMM + per-token epilogue; core; out-projection
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t stream);

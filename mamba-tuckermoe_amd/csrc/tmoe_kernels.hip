@@ -371,18 +371,24 @@ bool small_epi_fused_ok(const FwdArgs& a) {
   return stat + dev::sk_epi_dyn_bytes(mf, a) <= (size_t)160 * 1024 && a.r3 % 8 == 0;
 }
 
-bool small_decode_ok(const FwdArgs& a, hipStream_t st) {
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+}
+
+bool small_decode_shape_ok(const FwdArgs& a) {
   if (a.dtype != kDtypeBF16 || a.T > kDecodeMaxT || a.T * a.r3 > 16384 || a.E > 16 ||
       (a.r3 != 64 && a.r3 != 128 && a.r3 != 256) || !a.sync || a.r1 > 32)
     return false;
   const int mf = small_mf(a.T);
   const size_t stat = (size_t)mf * 256 * (1 + kSkW) * sizeof(float);   // SkLds<MF, kSkW>
-  if (stat + dev::sk_decode_dyn_bytes(mf, a) > (size_t)160 * 1024) return false;
+  return stat + dev::sk_decode_dyn_bytes(mf, a) <= (size_t)160 * 1024;
+}
+
+bool small_decode_ok(const FwdArgs& a, hipStream_t st) {
   // the consumers wait on flags that stay set (several per flag): a replayed graph
   // would find them set, so a captured forward takes the two-launch path
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
-  return true;
+  return small_decode_shape_ok(a) && !stream_capturing(st);
 }
 
 template <int MF>
@@ -487,18 +493,19 @@ hipError_t launch_fold_out_t(const uint16_t* coreT, const uint16_t* uoutT, const
 // 256 x 288 tile per work-group (T >= 8192 at d_out = 2304), on a device of 256
 // compute units (8 XCDs of 32), with the workspace's signal words, and not under
 // graph capture (its flags have several consumers and stay set).
-bool fused_large_ok(const FwdArgs& a, hipStream_t st) {
+bool fused_large_shape_ok(const FwdArgs& a) {
   if (a.dtype != kDtypeBF16 || !a.cz || !a.wfrag || a.r3 != 256 || a.E_pad != 32 || !a.sync)
     return false;
   if (!outproj_tiled_ok(a) || a.r2 % 64) return false;
   const int64_t tiles = (int64_t)cdiv(a.T, dev::wide::BM) * (a.d_out / dev::wide::BN);
-  if (tiles < dev::fused::kGrid || cu_count() != dev::fused::kGrid) return false;
-  // a signal flag per 64-token front tile, within the workspace's flags (one per
-  // kSyncTileRows tokens), and the row count addressed in int
-  if (a.T > ((int64_t)1 << 30)) return false;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
-  return true;
+  // a signal flag per 64-token front tile fits the workspace's flags (one per
+  // kSyncTileRows tokens); rows are addressed in int
+  return tiles >= dev::fused::kGrid && cu_count() == dev::fused::kGrid &&
+         a.T <= ((int64_t)1 << 30);
+}
+
+bool fused_large_ok(const FwdArgs& a, hipStream_t st) {
+  return fused_large_shape_ok(a) && !stream_capturing(st);
 }
 
 hipError_t launch_fused_large(const FwdArgs& a, hipStream_t st) {
@@ -523,12 +530,7 @@ bool front_fuses_cz(const FwdArgs& a, hipStream_t st) {
   // (not under graph capture: a consumer that gave up on its flag would leave it
   // to be found set on a replay with the same epoch; the captured forward runs
   // k_expand_cz instead)
-  if (a.r3 == 256 && a.E_pad == 256) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-      return false;
-    return a.r1 <= 32 && a.sync != nullptr;
-  }
+  if (a.r3 == 256 && a.E_pad == 256) return a.r1 <= 32 && a.sync != nullptr && !stream_capturing(st);
   return a.r1 <= 32;
 }
 
