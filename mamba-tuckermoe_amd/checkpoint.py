@@ -65,12 +65,15 @@ def checkpoint_state_dict(obj) -> Dict[str, torch.Tensor]:
     return {str(k): v for k, v in raw.items() if torch.is_tensor(v)}
 
 
-def export_npz(src, path: str, prefix: str = "", compressed: bool = True) -> int:
-    """Writes the floating tensors of src (a state dict, a module, a checkpoint
-    dict, or the path of a torch checkpoint file, read with weights_only=True) to
-    the .npz at path as float32 arrays (bf16 / fp16 widened exactly), each key
-    prefixed with `prefix` (e.g. "backbone.layers.0.block.ffn.gate_proj." for one
-    layer's own state dict). Integer tensors (fp8 codes) keep their dtype. Returns
+def export_npz(src, path: str, prefix: str = "", compressed: bool = True,
+               keep_int: bool = False) -> int:
+    """Writes every tensor of src (a state dict, a module, a checkpoint dict, or the
+    path of a torch checkpoint file, read with weights_only=True) to the .npz at path
+    as a float32 array (bf16 / fp16 widened exactly), each key prefixed with `prefix`
+    (e.g. "backbone.layers.0.block.ffn.gate_proj." for one layer's own state dict).
+    As the reference's export step, integer and bool tensors are converted to float32
+    too (export_ckpt_to_npz.py:59-60: `.float()` on every tensor; fp8 codes 0..255 are
+    exact in float32); keep_int=True writes them in their own dtype instead. Returns
     the number of arrays written (export_ckpt_to_npz.py:43-66)."""
     if isinstance(src, (str, bytes)) or hasattr(src, "__fspath__"):
         src = torch.load(src, map_location="cpu", weights_only=True)
@@ -78,7 +81,7 @@ def export_npz(src, path: str, prefix: str = "", compressed: bool = True) -> int
     arrays = {}
     for k, t in sd.items():
         t = t.detach().cpu()
-        arrays[prefix + k] = (t.float() if t.is_floating_point() else t).numpy()
+        arrays[prefix + k] = (t if keep_int and not t.is_floating_point() else t.float()).numpy()
     (np.savez_compressed if compressed else np.savez)(path, **arrays)
     return len(arrays)
 

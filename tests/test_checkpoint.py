@@ -118,6 +118,25 @@ def test_export_npz_round_trip(pkg, tmp_path):
     assert all(np.array_equal(again[k], arrays[k]) for k in arrays)
 
 
+def test_export_npz_integer_tensors_as_float32(pkg, tmp_path):
+    """As the reference's export (export_ckpt_to_npz.py:59-60, `.float()` on every
+    tensor), integer and bool tensors are written as float32 with the same values
+    (fp8 codes 0..255 are exact); keep_int=True keeps their dtype."""
+    codes = torch.arange(256, dtype=torch.uint8)
+    sd = {"U_in_q": codes, "mask": torch.tensor([True, False]), "step": torch.tensor(7),
+          "w": torch.ones(3, dtype=torch.bfloat16)}
+    pkg.checkpoint.export_npz(sd, str(tmp_path / "a.npz"))
+    a = pkg.checkpoint.load_npz(str(tmp_path / "a.npz"))
+    assert all(v.dtype == np.float32 for v in a.values())
+    assert np.array_equal(a["U_in_q"], np.arange(256, dtype=np.float32))
+    assert np.array_equal(a["mask"], np.array([1.0, 0.0], dtype=np.float32))
+    assert a["step"] == 7.0
+    pkg.checkpoint.export_npz(sd, str(tmp_path / "b.npz"), keep_int=True)
+    b = pkg.checkpoint.load_npz(str(tmp_path / "b.npz"))
+    assert b["U_in_q"].dtype == np.uint8 and b["mask"].dtype == np.bool_
+    assert b["w"].dtype == np.float32
+
+
 class _Opaque:
     pass
 
