@@ -38,13 +38,20 @@ def log(*a):
 
 
 def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), with its family / model / stepping and
+    the number of online CPUs, which tell EPYC generations apart where the name is
+    generic."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info.setdefault(k.strip(), v.strip())
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    name = info.get("model name") or platform.processor() or "unknown"
+    extra = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(extra + [f'{os.cpu_count()} online CPUs'])})"
 
 
 def profile_figure(workload: str, key: str, stage: str):
@@ -303,7 +310,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="override T")
     ap.add_argument("--rotate-mb", type=float, default=640.0,
                     help="minimum total size of the rotated buffer sets")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+    ap.add_argument("--cpu-seconds", type=float, default=24.0,
                     help="approximate CPU work of the host baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
