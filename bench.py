@@ -322,6 +322,8 @@ def main():
                     help="keep the core and the out-projection as two GEMMs (TMOE_FLAG_NO_FOLD)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the extra workloads (C2, C4, C3 at T=2048 and T=1) of the C3 run")
+    ap.add_argument("--no-probes", action="store_true",
+                    help="skip the hardware probes and the vendor-library GEMM (C3 runs only)")
     ap.add_argument("--no-fuse", action="store_true",
                     help="never run the large-T forward as one launch (TMOE_FLAG_NO_FUSE)")
     ap.add_argument("--latent", action="store_true",
@@ -372,7 +374,66 @@ def main():
                 "parity": rr["parity"],
             }
         res["extra"] = extra
+    if not args.no_probes and args.workload == "C3" and not args.tokens:
+        res["probes"] = hw_probes(pkg, w, res)
     print(json.dumps(res), flush=True)
+
+
+def hw_probes(pkg, w, res) -> dict:
+    """What this MI355X sustains on the resources the layer's kernels are bound by
+    (include/tmoe_probe.h, libtmoe_probe.so), and the vendor library (hipBLASLt via
+    torch.matmul) on the layer's out-projection GEMM, measured in the same run. Not
+    part of the timed region; the headline and its roofline are unchanged by it."""
+    import ctypes
+
+    import torch
+    out = {}
+    lib_path = os.path.join(os.path.dirname(pkg._lib.LIB_PATH), "libtmoe_probe.so")
+    if os.path.exists(lib_path):
+        L = ctypes.CDLL(lib_path)
+        dp = ctypes.POINTER(ctypes.c_double)
+        L.tmoe_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, dp, dp]
+        L.tmoe_probe_l2_stream.argtypes = [ctypes.c_int, ctypes.c_int, dp]
+        for name, rnd in (("constant", 0), ("random", 1)):
+            tf, mhz = ctypes.c_double(), ctypes.c_double()
+            if L.tmoe_probe_mfma(rnd, 20000, ctypes.byref(tf), ctypes.byref(mhz)) == 0:
+                out[f"mfma_bf16_{name}_operands"] = {"tflops": tf.value, "frac_of_peak": tf.value / PEAK_TFLOPS["bf16"],
+                                                     "shader_mhz": mhz.value}
+        l2 = {}
+        for dma in (0, 1):
+            for waves in (4, 8):
+                g = ctypes.c_double()
+                if L.tmoe_probe_l2_stream(dma, waves, ctypes.byref(g)) == 0:
+                    l2[f"{'lds_dma' if dma else 'registers'}_{waves}_waves"] = g.value
+        out["l2_stream_gbs_per_cu"] = l2
+    else:
+        out["missing"] = lib_path
+    # hipBLASLt on the out-projection's GEMM: (T x K) x (K x d_out), bf16 in, fp32 accumulate
+    dev = torch.device("cuda:0")
+    K = w.r1 * w.r3 if res["config"]["form"] == "folded" else w.r2
+
+    def lib_gemm(M, N, Kd):
+        a = torch.randn(M, Kd, device=dev).to(torch.bfloat16)
+        b = torch.randn(Kd, N, device=dev).to(torch.bfloat16)
+        for _ in range(3):
+            a @ b
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                a @ b
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / 10 * 1e3
+            best = us if best is None else min(best, us)
+        return {"shape_mnk": [M, N, Kd], "us": best, "tflops": 2.0 * M * N * Kd / best * 1e-6}
+
+    out["hipblaslt_outproj_gemm"] = lib_gemm(res["config"]["T"], w.d_out, K)
+    out["hipblaslt_square_8192"] = lib_gemm(8192, 8192, 8192)
+    log(f"[probes] {json.dumps(out)}")
+    return out
 
 
 # the workloads measured beside the C3 headline: (key, workload, T or None)

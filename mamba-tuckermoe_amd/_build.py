@@ -17,6 +17,10 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libtmoe.so")
 
 SOURCES = ["tmoe_kernels.hip", "tmoe_static.hip", "tmoe_api.cpp"]
+# the measurement harness's hardware probes (include/tmoe_probe.h), a library of
+# their own so that libtmoe.so holds only the layer
+PROBE_SOURCES = ["tmoe_probe.hip"]
+PROBE_LIB = os.path.join(HERE, "libtmoe_probe.so")
 ARCH = "gfx950"
 
 # Packed FP32 vector instructions are disabled for all device code: hipcc -O3
@@ -42,22 +46,27 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles every source (concurrently) and links libtmoe.so; returns its path."""
+    """Compiles every source (concurrently) and links libtmoe.so and
+    libtmoe_probe.so; returns libtmoe.so's path."""
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs, cmds = [], []
-    for src in SOURCES:
-        obj = os.path.join(objdir, src + ".o")
-        lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmds.append([hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c",
-                     os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+    cmds, groups = [], []
+    for lib, sources in ((LIB, SOURCES), (PROBE_LIB, PROBE_SOURCES)):
+        objs = []
+        for src in sources:
+            obj = os.path.join(objdir, src + ".o")
+            lang = ["-x", "hip"] if src.endswith(".hip") else []
+            cmds.append([hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c",
+                         os.path.join(CSRC, src), "-o", obj])
+            objs.append(obj)
+        groups.append((lib, objs))
     _run_all(cmds, verbose)
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
-           "-Wl,-rpath,/opt/rocm/lib"]
-    _run(cmd, verbose)
-    os.replace(tmp, LIB)
+    for lib, objs in groups:
+        tmp = lib + ".tmp"
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+               "-Wl,-rpath,/opt/rocm/lib"]
+        _run(cmd, verbose)
+        os.replace(tmp, lib)
     return LIB
 
 

@@ -10,8 +10,8 @@ import torch
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _header_functions():
-    src = open(os.path.join(ROOT, "include", "tmoe.h")).read()
+def _header_functions(header="tmoe.h"):
+    src = open(os.path.join(ROOT, "include", header)).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"\b(tmoe_[a-z0-9_]+)\s*\(", src)))
 
@@ -22,6 +22,21 @@ def test_exports_every_header_symbol(pkg):
     assert set(declared) == set(pkg._lib.EXPORTED)
     for name in declared:
         assert hasattr(L, name), name
+
+
+def test_probe_library_exports_its_header(pkg):
+    """The measurement harness's probe library (bench.py's "probes") loads and
+    exports what include/tmoe_probe.h declares; a bad argument is refused on the
+    host."""
+    path = os.path.join(os.path.dirname(pkg._lib.LIB_PATH), "libtmoe_probe.so")
+    L = ctypes.CDLL(path)
+    declared = _header_functions("tmoe_probe.h")
+    assert declared == ["tmoe_probe_l2_stream", "tmoe_probe_mfma"]
+    for name in declared:
+        assert hasattr(L, name), name
+    L.tmoe_probe_l2_stream.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    g = ctypes.c_double()
+    assert L.tmoe_probe_l2_stream(0, 5, ctypes.byref(g)) == -1   # waves must be 4 or 8
 
 
 def test_abi_version(pkg):
