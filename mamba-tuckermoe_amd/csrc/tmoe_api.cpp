@@ -136,7 +136,8 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   const int64_t tile_rows = p->core_p || p->fold
                                 ? (T + tmoe::kCorePRows - 1) / tmoe::kCorePRows * tmoe::kCorePRows
                                 : T;
-  L.z = o;   o = align256(o + (size_t)T * p->s.r3 * p->es);
+  // z in whole tiles too: a folded plan's out-projection may read it as its A operand
+  L.z = o;   o = align256(o + (size_t)(p->fold ? tile_rows : T) * p->s.r3 * p->es);
   L.c = o;   o = align256(o + (size_t)tile_rows * p->rk * sizeof(float));
   L.idx = o; o = align256(o + (size_t)T * p->s.k * sizeof(int32_t));
   L.w = o;   o = align256(o + (size_t)T * p->s.k * sizeof(float));
@@ -239,7 +240,11 @@ tmoe::FwdArgs folded_args(const tmoe_plan* p, const tmoe::FwdArgs& a, const void
   f.r2 = p->rk * p->s.r3;
   f.uoutT = static_cast<const char*>(packed) + p->off_fold;
   f.out_scale = nullptr;
-  f.cz = tmoe::front_fuses_cz(f, st) ? f.mid : nullptr;
+  // the out-projection forms c (x) z itself where it can (z and c from the
+  // front); else the front writes c (x) z into mid where it can, else
+  // k_expand_cz does
+  f.kr = tmoe::outproj_kr_ok(f);
+  f.cz = !f.kr && tmoe::front_fuses_cz(f, st) ? f.mid : nullptr;
   return f;
 }
 
@@ -266,9 +271,10 @@ void small_stages(const tmoe::FwdArgs& a, bool fold, hipStream_t stream, Launch 
   }
 }
 
-// stage 2 of a folded plan: c (x) z, unless the front already wrote it
+// stage 2 of a folded plan: c (x) z, unless the front already wrote it or the
+// out-projection forms it
 hipError_t launch_cz(const tmoe::FwdArgs& f, hipStream_t st) {
-  return f.cz ? hipSuccess : tmoe::launch_expand_cz(f, st);
+  return f.cz || f.kr ? hipSuccess : tmoe::launch_expand_cz(f, st);
 }
 
 }  // namespace

@@ -61,6 +61,10 @@ struct FwdArgs {
   bool mid_rows_256;            // mid is allocated for T rounded up to 256 rows
   void* cz;                     // folded plans whose front writes c (x) z itself (= mid;
                                 //                      then z is not stored), else null
+  bool kr;                      // folded plans whose out-projection forms c (x) z from z
+                                //                      and c in its loop (outproj_kr_ok):
+                                //                      no c (x) z is stored; z and c are
+                                //                      allocated for T rounded up to 256 rows
   float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
   float* mpart;                 // (S, T_pad, r2) fp32  k_core_pp with r1 > 4: partial sums
                                 //                      over rank groups (null otherwise)
@@ -230,6 +234,10 @@ hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t stream);
 // itself (a.cz): the single-kind front (not the K-sliced one nor the split one of
 // the widest routers) with at most 32 ranks. Then no launch_expand_cz is needed.
 bool front_fuses_cz(const FwdArgs& a, hipStream_t stream);
+// Folded bf16 plans (r1 = 4, r3 = 256, K = 1024, E_pad = 256) whose large-T
+// out-projection is k_outproj_wide: it forms c (x) z in its loop from the z and c
+// the front stores.
+bool outproj_kr_ok(const FwdArgs& a);
 // The whole large-T forward of a folded plan in one launch (k_fused_large): front
 // tiles and out-projection tiles in one persistent grid of one work-group per
 // compute unit, c (x) z handed over inside each XCD's L2. fused_large_ok: the plan,

@@ -199,6 +199,13 @@ bool outproj_tiled_ok(const FwdArgs& a) {
   return a.r2 % 64 == 0 && a.d_out % dev::wide::BN == 0 && a.mid_rows_256;
 }
 
+// The out-projection's 128 x 144 tiles (k_outproj_mid) number at most the compute
+// units: launch_outproj_bf16 takes k_outproj_mid, else k_outproj_wide.
+bool outproj_mid_tiles(const FwdArgs& a) {
+  return (int64_t)cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN) <= cu_count();
+}
+
+
 // bf16 out-projection: persistent, one work-group per compute unit (its LDS
 // holds one), each looping over the tiles b, b + grid, ...
 hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
@@ -215,10 +222,22 @@ hipError_t launch_outproj_bf16(const FwdArgs& a, hipStream_t st) {
     uint16_t* out = static_cast<uint16_t*>(a.out);
     const int T = (int)a.T, N = (int)a.d_out, K = (int)a.r2;
     const int64_t ntn = a.d_out / dev::wide::BN;
-    const int64_t t_mid = cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN);
     const int64_t t128 = cdiv(a.T, dev::wide::Cfg<1>::BM) * ntn;
     const int64_t t256 = cdiv(a.T, dev::wide::Cfg<2>::BM) * ntn;
-    if (t_mid <= ncu) {
+    if (a.kr) {   // A = c (x) z formed from z and c in the loop (outproj_kr_ok)
+      const uint16_t* Z = static_cast<const uint16_t*>(a.z);
+      if (t128 <= ncu) {
+        hipLaunchKernelGGL(dev::k_outproj_wide_kr<1>, dim3((unsigned)t128), dim3(256), 0, st, Z,
+                           a.c, Bt, out, a.bias, T, N, K);
+      } else {
+        const dim3 grid((unsigned)(t256 < ncu ? t256 : ncu));
+        hipLaunchKernelGGL(dev::k_outproj_wide_kr<2>, grid, dim3(256), 0, st, Z, a.c, Bt, out,
+                           a.bias, T, N, K);
+      }
+      return hipGetLastError();
+    }
+    if (outproj_mid_tiles(a)) {
+      const int64_t t_mid = cdiv(a.T, dev::mid::BM) * (a.d_out / dev::mid::BN);
       hipLaunchKernelGGL(dev::k_outproj_mid, dim3((unsigned)t_mid), dim3(256), 0, st, A, Bt, out,
                          a.bias, T, N, K);
     } else if (t128 <= ncu) {
@@ -353,6 +372,20 @@ struct SmallOutKR {
 };
 
 }  // namespace
+
+bool outproj_kr_ok(const FwdArgs& a) {
+  // Only where the front cannot write c (x) z without a hand-off: the split front
+  // of the widest routers (E_pad = 256: z and the router in different work-groups)
+  // would make its z work-groups wait for c (or a separate k_expand_cz pass run).
+  // Elsewhere the front's own c (x) z stores cost about what the scaling costs the
+  // loop (C3, two launches: front 38.8 -> 31.9 us, out-projection 83.9 -> 91.1 us;
+  // the one-launch forward 116.2 -> 121.2 us), while C4 gains ~4 us.
+  // Every large-T front stores z (bf16) and c (fp32) when a.cz is unset; z and c
+  // are allocated in whole 256-row tiles (a.mid_rows_256: the folded layout).
+  return a.T > kSmallT && outproj_tiled_ok(a) && a.E_pad > 128 && a.r1 == dev::wide::kKrR1 &&
+         a.r3 == dev::wide::kKrR3 && a.r2 == dev::wide::kKrR1 * dev::wide::kKrR3 &&
+         !outproj_mid_tiles(a);
+}
 
 hipError_t launch_small_front(const FwdArgs& a, hipStream_t st) { return by_rows<SmallFront>(a, st); }
 hipError_t launch_small_core(const FwdArgs& a, hipStream_t st) { return by_rows<SmallCore>(a, st); }

@@ -20,10 +20,19 @@
 // under the next tile's first K tiles. The bias columns come through the
 // scalar unit (no LDS read after the DMA, which would wait for it).
 //
+// The A operand is either stored rows of K elements (mid, or c (x) z written by
+// the front), or, for folded plans with r1 = 4 and r3 = 256 (KR), formed in the
+// loop: the DMA brings z's rows (r3 = 256 elements) into the A part of a stage,
+// K tile kt reading z's columns 64 (kt % 4) .. and belonging to rank r = kt / 4,
+// and each A fragment is scaled by its row's c_r on its way from LDS to the
+// MFMA, R(c_r R(z)) exactly as the front would have stored it. A stage then
+// holds a quarter of the A bytes it would otherwise (z instead of c (x) z), and
+// the 4x larger c (x) z is never written.
+//
 // Shape contract (checked by the host): K % 64 == 0, N % 288 == 0 (W^T rows
-// read in whole tiles), A allocated for T rounded up to 256 rows (rows past T
-// are read, their results never stored), no column scale and no fused
-// epilogue.
+// read in whole tiles), A (or z and c) allocated for T rounded up to 256 rows
+// (rows past T are read, their results never stored), no column scale and no
+// fused epilogue; KR: K = 4 * 256.
 #pragma once
 
 namespace tmoe {
@@ -53,6 +62,17 @@ struct Cfg {
 };
 constexpr int BM = Cfg<2>::BM;   // the large-T tile
 
+constexpr int kKrR1 = 4, kKrR3 = 256;   // the KR operand's ranks
+constexpr int kKrTilesPerRank = kKrR3 / 64;
+// Fragment steps of a K step: A fragment reads at steps 0 .. FM - 1, W^T fragment
+// reads at FM .. FM + FN - 1; with the KR operand, dword d of A fragment i is
+// scaled at step kKrScale0 + 4 i + d (four MFMAs after the A reads, one 16-byte
+// group's 5 VALU instructions per MFMA gap)
+constexpr int kKrScale0 = 4;
+constexpr int frag_steps(int fm) {
+  return fm + FN > kKrScale0 + 4 * fm ? fm + FN : kKrScale0 + 4 * fm;
+}
+
 }  // namespace wide
 
 #define TMOE_MFMA_A(acc, b, a) \
@@ -67,7 +87,8 @@ constexpr int BM = Cfg<2>::BM;   // the large-T tile
 // One K step (16 of K) of a wave's 18 blocks, W^T fragment first (transposed
 // result: lane l holds row l & 31 of the block and columns 8 q + 4 (l >> 5) +
 // 0..3 in elements 4 q .. 4 q + 3). ld(b) runs after the b-th MFMA: the next
-// step's fragment reads, spread between the MFMAs.
+// step's fragment reads and (KR operand) the scaling of its A fragments, spread
+// between the MFMAs (wide::frag_steps(FM) steps b in all).
 template <bool kZero, int FM, class LD>
 __device__ __forceinline__ void wide_step(f32x16 (&acc)[FM][wide::FN], const u32x4 (&af)[FM],
                                           const u32x4 (&bf)[wide::FN], LD&& ld) {
@@ -86,22 +107,24 @@ __device__ __forceinline__ void wide_step(f32x16 (&acc)[FM][wide::FN], const u32
       ld(blk);
       __builtin_amdgcn_sched_barrier(0);
     }
-  // fewer MFMAs than fragments (FM = 1: 9 against 10): the rest after the last
+  // fewer MFMAs than fragment steps (FM = 1: 9 against 10): the rest after the last
 #pragma unroll
-  for (int m = FM * wide::FN; m < FM + wide::FN; ++m) ld(m);
+  for (int m = FM * wide::FN; m < wide::frag_steps(FM); ++m) ld(m);
 }
 
 // The tile loop of a work-group: out = A Bt^T + bias over the tiles a schedule
 // hands it. Sched: start(tm, tn) gives the first tile (false: none) and
 // advance(tm, tn) the next (false: no more), both called uniformly by the whole
 // work-group. A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32.
+// KR: A is z (M rows, 256) and cr is c (M rows, 4 floats), K = 1024.
 // smem: 2 Cfg<FM>::kStage 16-byte slots of LDS.
-template <int FM_, class Sched>
+template <int FM_, class Sched, bool KR = false>
 __device__ __forceinline__ void wide_loop(const uint16_t* __restrict__ A,
                                           const uint16_t* __restrict__ Bt,
                                           uint16_t* __restrict__ C,
                                           const float* __restrict__ bias, int M, int N, int K,
-                                          u32x4* smem, Sched& sched) {
+                                          u32x4* smem, Sched& sched,
+                                          const float* __restrict__ cr = nullptr) {
   using wide::FN;
   using wide::BN;
   using wide::kAgprBlk;
@@ -113,42 +136,87 @@ __device__ __forceinline__ void wide_loop(const uint16_t* __restrict__ A,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nkt = K / 64;
   const uint32_t row_bytes = (uint32_t)K * 2;
+  const uint32_t a_row_bytes = KR ? (uint32_t)wide::kKrR3 * 2 : row_bytes;
 
   f32x16 acc[FM][FN];
   u32x4 fa[2][FM], fb[2][FN];
+  // KR: c (all 4 ranks) of this lane's row in the wave's row blocks 0 and 1 (named
+  // registers: an array of them was kept in scratch memory)
+  float4 ca0 = {0.f, 0.f, 0.f, 0.f}, ca1 = {0.f, 0.f, 0.f, 0.f};
+  static_assert(FM <= 2, "KR: at most two row blocks per wave");
+  auto load_c = [&](int tm_) __attribute__((always_inline)) {
+    if constexpr (KR) {
+      const float* c0 = cr + (int64_t)(tm_ * BM + wave * (32 * FM) + (lane & 31)) * wide::kKrR1;
+      ca0 = *reinterpret_cast<const float4*>(c0);
+      if constexpr (FM > 1) ca1 = *reinterpret_cast<const float4*>(c0 + 32 * wide::kKrR1);
+    }
+  };
+  // c_r of row block m for K tile kt (rank kt / 4), by selects
+  auto c_of = [&](int m, int kt) __attribute__((always_inline)) -> float {
+    const int r = kt / wide::kKrTilesPerRank;
+    const float4 v = m == 0 ? ca0 : ca1;
+    return r == 0 ? v.x : r == 1 ? v.y : r == 2 ? v.z : v.w;
+  };
 
   int tm, tn;
   if (!sched.start(tm, tn)) return;
+  load_c(tm);
 
   // DMA block wave + 4 d of a stage: A rows 32 d + 8 wave + (lane >> 3) for
   // d < kABlocksPerWave, else W^T rows 32 (d - kABlocksPerWave) + 8 wave +
   // (lane >> 3). Whole tiles are in bounds, so one per-lane offset serves all.
   const uint32_t voff = (uint32_t)(8 * wave + (lane >> 3)) * row_bytes +
                         (uint32_t)dma_chunk(lane, wave) * 16u;
+  const uint32_t voff_a = KR ? (uint32_t)(8 * wave + (lane >> 3)) * a_row_bytes +
+                                   (uint32_t)dma_chunk(lane, wave) * 16u
+                             : voff;
   auto dma = [&](int d, int kt, int stage, int tm_, int tn_) __attribute__((always_inline)) {
     const char* base;
-    if (d < kABlocksPerWave)
-      base = reinterpret_cast<const char*>(A) + (int64_t)tm_ * BM * row_bytes +
-             (int64_t)d * 32 * row_bytes;
-    else
+    uint32_t off;
+    if (d < kABlocksPerWave) {
+      base = reinterpret_cast<const char*>(A) + (int64_t)tm_ * BM * a_row_bytes +
+             (int64_t)d * 32 * a_row_bytes +
+             (KR ? kt % wide::kKrTilesPerRank : kt) * kTileKBytes;
+      off = voff_a;
+    } else {
       base = reinterpret_cast<const char*>(Bt) + (int64_t)tn_ * BN * row_bytes +
-             (int64_t)(d - kABlocksPerWave) * 32 * row_bytes;
-    base += kt * kTileKBytes;
+             (int64_t)(d - kABlocksPerWave) * 32 * row_bytes + kt * kTileKBytes;
+      off = voff;
+    }
     // the LDS address goes through an integer, as in the measured build of this
     // loop (a pointer with provenance changes the compiler's DMA alias tracking)
     const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) u32x4*)(
         smem + stage * kStage + (wave + 4 * d) * 64);
-    __builtin_amdgcn_global_load_lds((gbl_cvptr)(base + voff), (lds_vptr)(size_t)lds, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gbl_cvptr)(base + off), (lds_vptr)(size_t)lds, 16, 0, 0);
   };
+  // fragment step m of K step ks of K tile kt into buffer buf (see frag_steps):
+  // m < FM reads A fragment m (KR: its raw z into ra[m]), FM <= m < FM + FN reads
+  // W^T fragment m - FM, and (KR) step kKrScale0 + 4 i + d scales dword d of A
+  // fragment i, R(c_r R(z)) as the front's flush_cz forms it
+  u32x4 ra[FM];
   auto read_frag = [&](int kt, int ks, int buf, int m) __attribute__((always_inline)) {
     const u32x4* s = smem + (kt & 1) * kStage;
     const int ch = ks * 2 + (lane >> 5);
-    if (m < FM) fa[buf][m] = s[lds_slot(wave * (32 * FM) + m * 32 + (lane & 31), ch)];
-    else if (m < FM + FN) fb[buf][m - FM] = s[lds_slot(BM + (m - FM) * 32 + (lane & 31), ch)];
+    if (m < FM) {
+      const u32x4 v = s[lds_slot(wave * (32 * FM) + m * 32 + (lane & 31), ch)];
+      if constexpr (KR) ra[m] = v;
+      else fa[buf][m] = v;
+    } else if (m < FM + FN) {
+      fb[buf][m - FM] = s[lds_slot(BM + (m - FM) * 32 + (lane & 31), ch)];
+    }
+    if constexpr (KR) {
+      const int q = m - wide::kKrScale0;
+      if (q >= 0 && q < 4 * FM) {
+        const int i = q / 4, d = q % 4;
+        const float c = c_of(i, kt);
+        fa[buf][i][d] = pack_bf16x2(bf16_bits_to_f32(ra[i][d] & 0xffffu) * c,
+                                    bf16_bits_to_f32(ra[i][d] >> 16) * c);
+      }
+    }
   };
   auto read_frags = [&](int kt, int ks, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int m = 0; m < FM + FN; ++m) read_frag(kt, ks, buf, m);
+    for (int m = 0; m < wide::frag_steps(FM); ++m) read_frag(kt, ks, buf, m);
   };
 
   // One K tile: the MFMAs of its 4 K steps from fragments read one step ahead;
@@ -210,6 +278,9 @@ __device__ __forceinline__ void wide_loop(const uint16_t* __restrict__ A,
     int tm2 = tm, tn2 = tn;
     const bool has_next = sched.advance(tm2, tn2);
     const bool early = has_next && nkt > 1;
+    // the next tile's c (every A fragment of this tile has been read): older than
+    // its DMAs, so the counted waits below also cover it
+    if (has_next) load_c(tm2);
     if (has_next) {
 #pragma unroll
       for (int d = 0; d < kDmaPerWave; ++d) dma(d, 0, 0, tm2, tn2);
@@ -321,6 +392,21 @@ __global__ __launch_bounds__(256) void k_outproj_wide(const uint16_t* __restrict
   __shared__ u32x4 smem[2 * Cf::kStage];
   WideGridSched sched{0, N / wide::BN, ((M + Cf::BM - 1) / Cf::BM) * (N / wide::BN)};
   wide_loop<FM_>(A, Bt, C, bias, M, N, K, smem, sched);
+}
+
+// The same GEMM with the KR operand: A = c (x) z formed from z (M, 256) and c
+// (M, 4) in the loop, K = 1024.
+template <int FM_>
+__global__ __launch_bounds__(256) void k_outproj_wide_kr(const uint16_t* __restrict__ Z,
+                                                         const float* __restrict__ c,
+                                                         const uint16_t* __restrict__ Bt,
+                                                         uint16_t* __restrict__ C,
+                                                         const float* __restrict__ bias, int M,
+                                                         int N, int K) {
+  typedef wide::Cfg<FM_> Cf;
+  __shared__ u32x4 smem[2 * Cf::kStage];
+  WideGridSched sched{0, N / wide::BN, ((M + Cf::BM - 1) / Cf::BM) * (N / wide::BN)};
+  wide_loop<FM_, WideGridSched, true>(Z, Bt, C, bias, M, N, K, smem, sched, c);
 }
 
 #undef TMOE_MFMA_A
