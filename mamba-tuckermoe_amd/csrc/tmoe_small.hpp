@@ -403,9 +403,18 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
 
 // The Khatri-Rao A operand from z and c rows staged in LDS (SkKhatriRao's
 // arithmetic: A[t, r r3 + s] = R(c[t, r] z[t, s])).
+// LDS row stride (elements) of the z rows a Khatri-Rao GEMM reads: r3 plus 16
+// bytes. The GEMM's 16 lanes of a fragment read 16 rows at one K offset; with
+// rows a multiple of 256 bytes apart (r3 = 128, 256 bf16) they all hit the same
+// bank group (16-way conflicts), 16 bytes more puts them on 16 different ones.
+template <class T>
+__device__ __host__ constexpr int sk_z_stride(int r3) {
+  return r3 + 16 / (int)sizeof(T);
+}
+
 template <class Elt>
 struct SkKhatriRaoLds {
-  const typename Elt::T* z;   // (MF 16, r3)
+  const typename Elt::T* z;   // (MF 16, r3), rows sk_z_stride(r3) elements apart
   const float* c;             // (MF 16, r1)
   int r1, r3, rows_valid;
   __device__ __forceinline__ u32x4 chunk(int row, int64_t k) const {
@@ -413,7 +422,7 @@ struct SkKhatriRaoLds {
     const int t = row < rows_valid ? row : rows_valid - 1;
     // 32-bit division (k < r1 r3 < 2^31): the 64-bit one is a long inlined routine
     const int r = (int)((uint32_t)k / (uint32_t)r3), s = (int)k - r * r3;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(z + t * r3 + s);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(z + t * sk_z_stride<T>(r3) + s);
     const float cc = c[t * r1 + r];
     u32x4 o;
     if constexpr (sizeof(T) == 2) {
@@ -431,7 +440,8 @@ struct SkKhatriRaoLds {
 // Dynamic LDS bytes of k_sk_epi_gemm: z rows, c rows, U_expert.
 inline size_t sk_epi_dyn_bytes(int mf, const FwdArgs& a) {
   const size_t es = a.dtype == 1 ? 2 : 4;   // TMOE_BF16: 2-byte elements
-  return (size_t)mf * 16 * a.r3 * es + (size_t)mf * 16 * a.r1 * 4 + (size_t)a.E * a.r1 * 4;
+  const size_t zs = es == 2 ? sk_z_stride<uint16_t>((int)a.r3) : sk_z_stride<float>((int)a.r3);
+  return (size_t)mf * 16 * zs * es + (size_t)mf * 16 * a.r1 * 4 + (size_t)a.E * a.r1 * 4;
 }
 
 // The front epilogue fused into the Khatri-Rao GEMM that follows it (small T, raw
@@ -448,8 +458,9 @@ __global__ __launch_bounds__(64 * W) void k_sk_epi_gemm(FwdArgs a) {
   extern __shared__ u32x4 dynv[];   // 16-byte aligned: z rows are read as 16-byte chunks
   float* dyn = reinterpret_cast<float*>(dynv);
   const int R3 = (int)a.r3, R1 = (int)a.r1, E = (int)a.E;
-  T* zl = reinterpret_cast<T*>(dyn);                       // (MF 16, r3)
-  float* cl = reinterpret_cast<float*>(zl + MF * 16 * R3);   // (MF 16, r1)
+  const int ZS = sk_z_stride<T>(R3);
+  T* zl = reinterpret_cast<T*>(dyn);                       // (MF 16, r3), row stride ZS
+  float* cl = reinterpret_cast<float*>(zl + MF * 16 * ZS);   // (MF 16, r1)
   float* ue = cl + MF * 16 * R1;                             // (E, r1)
   const int64_t n0 = (int64_t)blockIdx.x * 16, m0 = (int64_t)blockIdx.y * MF * 16;
   const int rows_valid = (int)(a.T - m0 < MF * 16 ? a.T - m0 : MF * 16);
@@ -477,7 +488,7 @@ __global__ __launch_bounds__(64 * W) void k_sk_epi_gemm(FwdArgs a) {
   for (int i = 0; i < TPW; ++i) {
     const int row = wave + W * i;
     if (row < rows_valid)
-      epi_finish<Elt>(a, m0 + row, lane, L[i], ue, routing, false, zl + row * R3, cl + row * R1);
+      epi_finish<Elt>(a, m0 + row, lane, L[i], ue, routing, false, zl + row * ZS, cl + row * R1);
   }
   __syncthreads();
   SkKhatriRaoLds<Elt> as{zl, cl, R1, R3, rows_valid};
@@ -541,7 +552,7 @@ constexpr int kDecodeGroups = 4;
 inline size_t sk_decode_dyn_bytes(int mf, const FwdArgs& a) {
   const size_t rows = (size_t)mf * 16;
   const size_t router = ((size_t)a.E * a.r1 + 16 * a.r1) * 4;
-  const size_t consumer = rows * a.r3 * 2 + rows * a.r1 * 4;
+  const size_t consumer = rows * sk_z_stride<uint16_t>((int)a.r3) * 2 + rows * a.r1 * 4;
   return router > consumer ? router : consumer;
 }
 
@@ -698,8 +709,9 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
     return;
   }
   // ---- consumers: 16 columns of out = (c (x) z) W^T + bias ----
-  T* zl = reinterpret_cast<T*>(dyn);                          // (MF 16, r3)
-  float* cl = reinterpret_cast<float*>(zl + MF * 16 * R3);    // (MF 16, r1)
+  const int ZS = sk_z_stride<T>(R3);
+  T* zl = reinterpret_cast<T*>(dyn);                          // (MF 16, r3), row stride ZS
+  float* cl = reinterpret_cast<float*>(zl + MF * 16 * ZS);    // (MF 16, r1)
   const int64_t n0 = (int64_t)(bid - NP) * 16;
   const int64_t K = (int64_t)R1 * R3;
   const int64_t rb = K * (int64_t)sizeof(T);
@@ -745,8 +757,9 @@ __global__ __launch_bounds__(64 * W) void k_sk_decode(FwdArgs a) {
     const float ir = 1.f / sqrtf(ss / (float)R3 + a.eps);
     if (g < NG) {
       // z as stored by epi_finish: R((z / rms) * gain)
+      T* zrow = zl + (g / G) * ZS + (g - (g / G) * G) * 4;   // token g / G, columns 4 (g % G)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) store_from_f32(zl + g * 4 + q, (zv[j][q] * ir) * gv[j][q]);
+      for (int q = 0; q < 4; ++q) store_from_f32(zrow + q, (zv[j][q] * ir) * gv[j][q]);
     }
   }
   __syncthreads();
