@@ -539,7 +539,9 @@ def measure(pkg, w, args, *, steps, warmup, rotate_mb, no_fold, no_fuse, cpu, la
     fl_algo = w.flops()
     fl = w.flops_executed(T, rk, folded)        # the dominant kernel's own work
     fl["front"] = fl["router"] + fl["in_proj"]   # one kernel computes both
-    sb = w.stage_bytes_folded(T, rk) if folded else w.stage_bytes()
+    kr = path == pkg._lib.TMOE_PATH_LARGE_KR
+    sb = (w.stage_bytes_kr(T, rk) if kr else
+          w.stage_bytes_folded(T, rk) if folded else w.stage_bytes())
     one_launch = path in (pkg._lib.TMOE_PATH_DECODE, pkg._lib.TMOE_PATH_FUSED)
     kname = {pkg._lib.TMOE_PATH_DECODE: "k_sk_decode", pkg._lib.TMOE_PATH_FUSED: "k_fused_large"}
     if one_launch:
@@ -576,7 +578,7 @@ def measure(pkg, w, args, *, steps, warmup, rotate_mb, no_fold, no_fuse, cpu, la
 
     full_size = T == pkg.WORKLOADS[w.name].T
     stage_key = dom + ("_fused" if path == pkg._lib.TMOE_PATH_FUSED else
-                       "_folded" if folded else "")
+                       "_kr" if kr else "_folded" if folded else "")
     traffic = traffic_per_launch(w.name, stage_key) if full_size else None
     # MFMA-busy share of the dominant stage from the committed counter pass (the
     # timing-derived share is `frac`: executed flops / avg duration / peak at 2.4 GHz)

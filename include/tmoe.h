@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 10
+#define TMOE_ABI_VERSION 11
 
 /* error codes */
 #define TMOE_OK            0
@@ -253,6 +253,8 @@ int tmoe_forward_static(const tmoe_plan* plan, const void* x, int64_t T, const v
 #define TMOE_PATH_DECODE 2  /* T <= 64, bf16, folded: the whole layer in one launch   */
 #define TMOE_PATH_LARGE  3  /* front, (core or c (x) z), out-projection launches      */
 #define TMOE_PATH_FUSED  4  /* large T, folded: the whole layer in one launch         */
+#define TMOE_PATH_LARGE_KR 5 /* large T, folded, E > 128: front (stores z and c) and an
+                               out-projection that forms c (x) z in its loop            */
 int tmoe_forward_path(const tmoe_plan* plan, int64_t T);
 
 /* Lost in-launch signals. No counterpart in the reference (its forward has no

@@ -115,6 +115,20 @@ class Workload:
         st["out_proj"] = T * K * 2 + self.d_out * K * 2 + 4 * self.d_out + T * self.d_out * 2
         return st
 
+    def stage_bytes_kr(self, T: Optional[int] = None, rk: Optional[int] = None) -> dict:
+        """stage_bytes of a folded forward whose out-projection forms c (x) z itself
+        (TMOE_PATH_LARGE_KR): the front writes z and c (stage_bytes' front), there is
+        no core stage, and the out-projection reads z, c and W^T (d_out, rk*r3)."""
+        T = self.T if T is None else T
+        rk = self.r1 if rk is None else rk
+        st = self.stage_bytes(T)
+        es = 4 if self.dtype == torch.float32 else 2
+        K = rk * self.r3
+        st["core"] = 0
+        st["out_proj"] = (T * self.r3 * es + T * rk * 4 + self.d_out * K * 2 + 4 * self.d_out
+                          + T * self.d_out * es)
+        return st
+
     def one_launch(self, T: int, rk: int, folded: bool) -> bool:
         """Whether a forward of T tokens is the library's single decode launch
         (k_sk_decode; the selection rule of small_decode_ok in tmoe_kernels.hip,

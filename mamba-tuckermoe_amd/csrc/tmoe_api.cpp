@@ -830,9 +830,11 @@ int tmoe_forward_path(const tmoe_plan* p, int64_t T) {
     }
     return TMOE_PATH_SMALL;
   }
-  if (p->fold && !(p->s.flags & TMOE_FLAG_NO_FUSE) &&
-      tmoe::fused_large_shape_ok(folded_args(p, a, fake, nullptr)))
-    return TMOE_PATH_FUSED;
+  if (p->fold) {
+    const tmoe::FwdArgs f = folded_args(p, a, fake, nullptr);
+    if (!(p->s.flags & TMOE_FLAG_NO_FUSE) && tmoe::fused_large_shape_ok(f)) return TMOE_PATH_FUSED;
+    if (f.kr) return TMOE_PATH_LARGE_KR;
+  }
   return TMOE_PATH_LARGE;
 }
 

@@ -358,3 +358,20 @@ def test_plan_flags(pkg, flags, ok):
     finally:
         if p.value:
             pkg._lib.lib().tmoe_plan_destroy(p)
+
+
+def test_forward_path_rules(pkg):
+    """tmoe_forward_path's host-side selection (no GPU: as on a 256-compute-unit
+    MI355X): decode in one launch, the one-launch large-T forward, the wide-router
+    forward whose out-projection forms c (x) z itself, and the plain launches."""
+    cases = [("C2", 32, pkg._lib.TMOE_PATH_DECODE), ("C3", 16384, pkg._lib.TMOE_PATH_FUSED),
+             ("C5", 16384, pkg._lib.TMOE_PATH_FUSED), ("C3", 4096, pkg._lib.TMOE_PATH_LARGE),
+             ("C4", 4096, pkg._lib.TMOE_PATH_LARGE_KR), ("C4", 600, pkg._lib.TMOE_PATH_LARGE),
+             ("C3", 200, pkg._lib.TMOE_PATH_SMALL)]
+    for name, T, want in cases:
+        w = pkg.WORKLOADS[name]
+        m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(w.dtype)
+        assert m.plan().forward_path(T) == want, (name, T)
+    w = pkg.WORKLOADS["C4"]
+    m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(w.dtype).set_fold(False)
+    assert m.plan().forward_path(4096) == pkg._lib.TMOE_PATH_LARGE   # unfolded: no c (x) z
