@@ -1414,27 +1414,35 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
 // plane order and runs the per-token epilogue (RMSNorm, top-k, softmax, c).
 template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
           int WMF = kFrontWM>
-__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front_part(
-    FwdArgs a, float* __restrict__ raw, int nslices) {
-  typedef typename Elt::T T;
-  constexpr int EP = 32 * NR;
-  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
-  constexpr int NWT = NW * WMF;
+struct FrontPartGeom {
+  static constexpr int EP = 32 * NR;
+  static constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
+  static constexpr int NWT = NW * WMF;
   typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
+  typedef RouterExtra<Elt, TL::FM, NR, NW> RX;
+  static constexpr int LD = EP + 1;
+  static constexpr int kPlanes = RX::kSplitK ? NW : 1;
+  static constexpr int kSmemBytes = cmax(TL::kLdsBytes, kPlanes * BM * LD * 4);
+};
+
+// K slice `sl` of nslices of front tile `tile` (the work of one k_front_part
+// work-group): smem holds FrontPartGeom::kSmemBytes of LDS.
+template <class Elt, int R3, int NR, int PFA, int BM, int NS, int WMF>
+__device__ __forceinline__ void front_part_tile(const FwdArgs& a, float* __restrict__ raw,
+                                                int nslices, int tile, int sl, u32x4* smem) {
+  typedef typename Elt::T T;
+  typedef FrontPartGeom<Elt, R3, NR, PFA, BM, NS, WMF> G;
+  constexpr int EP = G::EP, NW = G::NW, LD = G::LD, kPlanes = G::kPlanes;
+  typedef typename G::TL TL;
+  typedef typename G::RX RX;
   constexpr int FM = TL::FM;
-  typedef RouterExtra<Elt, FM, NR, NW> RX;
-  constexpr int LD = EP + 1;
-  constexpr int kPlanes = RX::kSplitK ? NW : 1;
-  constexpr int kSmemBytes = cmax(TL::kLdsBytes, kPlanes * BM * LD * 4);
-  __shared__ u32x4 smem[kSmemBytes / 16];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wn = wave % NW, wrow = (wave / NW) * TL::kWaveM;
-  const int64_t m0 = (int64_t)blockIdx.x * BM;
+  const int64_t m0 = (int64_t)tile * BM;
   const int rows_valid = (int)(a.T - m0 < BM ? a.T - m0 : BM);
   const int64_t row_bytes = a.d_in * (int64_t)sizeof(T);
   const int nkt = (int)(row_bytes / kTileKBytes);
-  const int sl = (int)blockIdx.y;
   const int kt0 = sl * nkt / nslices, kt1 = (sl + 1) * nkt / nslices;
   RowLoader al{reinterpret_cast<const char*>(a.x) + m0 * row_bytes + (int64_t)kt0 * kTileKBytes,
                row_bytes, rows_valid};
@@ -1485,6 +1493,16 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
       plane[(int64_t)row * W + R3 + c] = v;
     }
   }
+}
+
+template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
+          int WMF = kFrontWM>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front_part(
+    FwdArgs a, float* __restrict__ raw, int nslices) {
+  typedef FrontPartGeom<Elt, R3, NR, PFA, BM, NS, WMF> G;
+  __shared__ u32x4 smem[G::kSmemBytes / 16];
+  front_part_tile<Elt, R3, NR, PFA, BM, NS, WMF>(a, raw, nslices, (int)blockIdx.x,
+                                                 (int)blockIdx.y, smem);
 }
 
 // The front for wide routers (E_pad = 32 NR > 128 with r3 = R3 = 256), in two kinds

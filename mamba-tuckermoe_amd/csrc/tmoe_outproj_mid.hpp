@@ -32,13 +32,45 @@ constexpr int kStage = kRows * 8;          // 16-byte slots per stage
 constexpr int kBlocks = kRows / 8;         // 34 DMA blocks of 8 rows
 constexpr int kABlocks = BM / 8;           // 16
 constexpr int kDmaPerWave = (kBlocks + 3) / 4;   // 9 (the last block repeats)
+constexpr int kFrags = FM + FN;            // fragment reads per K step
+constexpr int kSteps = FM * FN;            // MFMAs per K step
+constexpr int kDmaSlot0 = kSteps - kDmaPerWave;   // the MFMA a tile's first DMA follows
 static_assert(NS * kStage * 16 <= 160 * 1024, "LDS");
 static_assert((NS - 1) * kDmaPerWave <= 63, "vmcnt range");
+static_assert(kFrags <= kSteps && kDmaSlot0 >= 0, "reads and DMAs fit between the MFMAs");
 
 }  // namespace mid
 
 typedef float f32x4m __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2m __attribute__((ext_vector_type(2)));
+
+// One K step (32 of K) of a wave's 2 x 9 blocks, W^T fragment first. ld(b) runs
+// after the b-th MFMA (the next step's fragment reads, DMAs), each MFMA and its
+// ld fenced so that the compiler keeps them interleaved (left to itself it read
+// two fragments, waited for them, ran their MFMAs and so on: ~3x the MFMA time).
+// kZero: the accumulators' first step (C = 0), so that no instruction writes
+// them before an MFMA reads them (the compiler does not see these MFMAs and
+// would not keep the wait states such a write needs).
+template <bool kZero, class LD>
+__device__ __forceinline__ void mid_step(f32x4m (&acc)[mid::FM][mid::FN],
+                                         const u32x4 (&af)[mid::FM],
+                                         const u32x4 (&bf)[mid::FN], LD&& ld) {
+#pragma unroll
+  for (int j = 0; j < mid::FN; ++j)
+#pragma unroll
+    for (int i = 0; i < mid::FM; ++i) {
+      if (kZero)
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                     : "=a"(acc[i][j])
+                     : "v"(bf[j]), "v"(af[i]));
+      else
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                     : "+a"(acc[i][j])
+                     : "v"(bf[j]), "v"(af[i]));
+      ld(j * mid::FM + i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
 
 // A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32.
 __global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict__ A,
@@ -68,64 +100,79 @@ __global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict_
   // below kABlocks are A rows, the rest W^T rows
   const char* abase = reinterpret_cast<const char*>(A) + (int64_t)tm * BM * row_bytes;
   const char* bbase = reinterpret_cast<const char*>(Bt) + (int64_t)n0 * row_bytes;
-  auto dma = [&](int kt, int stage) __attribute__((always_inline)) {
+  auto dma_one = [&](int kt, int stage, int d) __attribute__((always_inline)) {
     u32x4* s = smem + stage * kStage;
-#pragma unroll
-    for (int d = 0; d < kDmaPerWave; ++d) {
-      const int blk = cmin_dev(wave + 4 * d, kBlocks - 1);
-      const int r = 8 * blk + (lane >> 3);   // stage row
-      const char* src = blk < kABlocks ? abase + (int64_t)r * row_bytes
-                                       : bbase + (int64_t)(r - BM) * row_bytes;
-      src += (int64_t)kt * kTileKBytes + dma_chunk(lane, blk) * 16;
-      // the LDS address goes through an integer (as in k_outproj_wide): with a
-      // pointer the compiler makes the fragment reads of the other stages wait for
-      // this DMA
-      const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) u32x4*)(s + blk * 64);
-      __builtin_amdgcn_global_load_lds((gbl_cvptr)src, (lds_vptr)(size_t)lds, 16, 0, 0);
-    }
+    const int blk = cmin_dev(wave + 4 * d, kBlocks - 1);
+    const int r = 8 * blk + (lane >> 3);   // stage row
+    const char* src = blk < kABlocks ? abase + (int64_t)r * row_bytes
+                                     : bbase + (int64_t)(r - BM) * row_bytes;
+    src += (int64_t)kt * kTileKBytes + dma_chunk(lane, blk) * 16;
+    // the LDS address goes through an integer (as in k_outproj_wide): with a
+    // pointer the compiler makes the fragment reads of the other stages wait for
+    // this DMA
+    const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) u32x4*)(s + blk * 64);
+    __builtin_amdgcn_global_load_lds((gbl_cvptr)src, (lds_vptr)(size_t)lds, 16, 0, 0);
   };
 
-  f32x4m acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4m{0.f, 0.f, 0.f, 0.f};
+  f32x4m acc[FM][FN];   // written first by tile 0's first K step (C = 0)
 
-  // prologue: tiles 0 .. NS - 2 in flight (those that exist)
+  // fragment b of K step ks (32 of K) of a stage: b < FM the wave's A rows, else
+  // the W^T rows of column block b - FM
+  u32x4 fa[2][FM], fb[2][FN];   // [0]: the tile's first K step, [1]: its second
+  auto frag = [&](const u32x4* s, int ks, int b, u32x4 (&af)[FM], u32x4 (&bf)[FN])
+      __attribute__((always_inline)) {
+    const int ch = ks * 4 + (lane >> 4);
+    if (b < FM) af[b] = s[lds_slot(wave * 32 + b * 16 + (lane & 15), ch)];
+    else bf[b - FM] = s[lds_slot(BM + (b - FM) * 16 + (lane & 15), ch)];
+  };
+
+  // prologue: tiles 0 .. NS - 2 in flight (those that exist), tile 0 landed, its
+  // first K step's fragments read
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
-    if (t < nkt) dma(t, t);
+    if (t < nkt)
+#pragma unroll
+      for (int d = 0; d < kDmaPerWave; ++d) dma_one(t, t, d);
+  static_assert(NS == 4, "the waits below count the tiles issued after the one awaited");
+  if (nkt > 2) wait_vm_lds<2 * kDmaPerWave>();
+  else if (nkt > 1) wait_vm_lds<kDmaPerWave>();
+  else wait_vm_lds<0>();
+  lds_barrier();
+#pragma unroll
+  for (int b = 0; b < kFrags; ++b) frag(smem, 0, b, fa[0], fb[0]);
 
-  static_assert(NS == 4, "the waits below count two tiles after tile kt");
+  // Each K tile: its first K step's MFMAs with the second step's fragment reads
+  // between them; the wait for tile kt + 1 and the barrier; the second step's
+  // MFMAs with tile kt + 1's first-step reads and the DMA of tile kt + NS - 1
+  // (into the stage tile kt - 1 used: every wave read it before this barrier)
+  // between them. Every iteration is the same code: past the last tile the
+  // reads fetch a stage no MFMA uses and the DMAs fetch the last tile again (in
+  // bounds, into a stage no later tile reads), so the wait has one count. With a
+  // branch or a peeled last tile the compiler copied accumulators between AGPRs
+  // right after the MFMAs that write them, which it cannot see through the
+  // MFMAs' asm statements (a read of an MFMA result needs wait states first).
   for (int kt = 0; kt < nkt; ++kt) {
-    // tile kt has landed once at most the DMAs of the tiles issued after it
-    // (kt + 1, kt + 2, as far as they exist) remain
-    if (kt + 2 < nkt) wait_vm_lds<2 * kDmaPerWave>();
-    else if (kt + 1 < nkt) wait_vm_lds<kDmaPerWave>();
-    else wait_vm_lds<0>();
-    lds_barrier();
-    // tile kt + NS - 1 into the stage tile kt - 1 used (every read of it ended
-    // before the barrier above)
-    if (kt + NS - 1 < nkt) dma(kt + NS - 1, (kt + NS - 1) % NS);
     const u32x4* s = smem + (kt % NS) * kStage;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int ch = ks * 4 + (lane >> 4);
-      u32x4 af[FM], bf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = s[lds_slot(wave * 32 + i * 16 + (lane & 15), ch)];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = s[lds_slot(BM + j * 16 + (lane & 15), ch)];
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, bf[j]), __builtin_bit_cast(bf16x8, af[i]), acc[i][j], 0,
-              0, 0);
-    }
+    auto ld1 = [&](int b) __attribute__((always_inline)) {
+      if (b < kFrags) frag(s, 1, b, fa[1], fb[1]);
+    };
+    if (kt == 0) mid_step<true>(acc, fa[0], fb[0], ld1);
+    else mid_step<false>(acc, fa[0], fb[0], ld1);
+    // tile kt + 1 has landed once at most the DMAs issued after it remain:
+    // those of iteration kt - 1 (tile kt + 2 or a repeat; in iteration 0 the
+    // prologue's tile 2, if there is one)
+    if (kt == 0 && nkt <= 2) wait_vm_lds<0>();
+    else wait_vm_lds<kDmaPerWave>();
+    lds_barrier();
+    const u32x4* sn = smem + ((kt + 1) % NS) * kStage;
+    const int kd = cmin_dev(kt + NS - 1, nkt - 1), sd = (kt + NS - 1) % NS;
+    mid_step<false>(acc, fa[1], fb[1], [&](int b) __attribute__((always_inline)) {
+      if (b < kFrags) frag(sn, 0, b, fa[0], fb[0]);
+      if (b >= kDmaSlot0) dma_one(kd, sd, b - kDmaSlot0);
+    });
   }
   mfma_drain();
+  wait_vm_lds<0>();   // the repeated DMAs land before the work-group's LDS is released
 
   // epilogue: lane l holds token 32 wave + 16 i + (l & 15), columns 16 j + 4 (l >> 4)
   // + 0..3: one 8-byte store per block
