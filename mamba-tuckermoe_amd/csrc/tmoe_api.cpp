@@ -148,7 +148,7 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   L.raw = o;
   L.fsplit = tmoe::front_split(T, p->s.d_in, p->E_pad, p->kdtype == TMOE_BF16);
   if (T <= tmoe::kSmallT || L.fsplit > 1) {
-    int64_t raw_floats = L.fsplit * T * (p->s.r3 + p->s.E);
+    int64_t raw_floats = L.fsplit * T * tmoe::raw_stride(p->s.r3, p->s.E);
     // the one-launch decode's scratch (z columns, sums of squares, c)
     if (T <= tmoe::kDecodeMaxT)
       raw_floats = std::max(raw_floats, tmoe::sk_decode_scratch_floats(T, p->s.r3, p->rk));
@@ -166,7 +166,9 @@ Layout workspace_layout(const tmoe_plan* p, int64_t T) {
   L.sync = o;
   if (T > 0)
     o = align256(o + (size_t)tmoe::sync_words(
-                             T, T <= tmoe::kDecodeMaxT ? tmoe::sk_decode_flags(p->s.r3) : 0) *
+                             T, std::max<int64_t>(T <= tmoe::kDecodeMaxT
+                                                      ? tmoe::sk_decode_flags(p->s.r3) : 0,
+                                                  tmoe::front_sliced_flags(T, L.fsplit))) *
                          sizeof(uint32_t));
   L.total = o;
   return L;
@@ -586,6 +588,8 @@ int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool small = T <= tmoe::kSmallT;
   const bool fold = p->fold;
+  // the K-sliced front in one launch where the device and the stream allow
+  a.front_one = !(p->s.flags & TMOE_FLAG_NO_FUSE) && tmoe::front_sliced_ok(a, st);
   if (fold) a = folded_args(p, a, packed, st);
   // the large-T folded forward in one launch where the plan, T and the device allow
   const bool fused = fold && !small && !(p->s.flags & TMOE_FLAG_NO_FUSE) &&

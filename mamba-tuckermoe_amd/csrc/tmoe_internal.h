@@ -65,12 +65,15 @@ struct FwdArgs {
                                 //                      and c in its loop (outproj_kr_ok):
                                 //                      no c (x) z is stored; z and c are
                                 //                      allocated for T rounded up to 256 rows
-  float* raw;                   // (T, r3 + E) fp32     small-T path: x [U_in | W_r^T]
+  float* raw;                   // (T, raw_stride) fp32 small-T path: x [U_in | W_r^T];
+                                //                      K-sliced front: front_split planes
   float* mpart;                 // (S, T_pad, r2) fp32  k_core_pp with r1 > 4: partial sums
                                 //                      over rank groups (null otherwise)
   int core_split;               // S: parts an output tile's rank groups are split into
   int front_split;              // K slices of the large-T front (raw holds that many
                                 //                      (T, r3 + E) fp32 planes), 1: none
+  bool front_one;               // front_split > 1: slices and epilogue in one launch
+                                //                      (k_front_sliced, front_sliced_ok)
   // elementwise op fused into the out-projection's store (kEpi*): the FFN
   // sub-block's silu(gate) * up, or its residual + LayerScale
   int epi_mode;
@@ -134,13 +137,17 @@ constexpr int64_t kCorePScales = 4096;
 inline bool core_p_grouped(int64_t r1) { return r1 > 4; }
 // K slices of the large-T bf16 front (router widths E_pad <= 128): when its
 // 64-token tiles number at most a quarter of kCoreUnits and d_in spans at least 16
-// K tiles, enough slices (of at least kFrontSliceKTiles each, at most kMaxFrontPlanes) to
-// approach kCoreUnits work-groups.
+// K tiles. The slices fill one XCD's 32 compute units with that XCD's tiles (tile
+// ft on XCD ft % 8, as k_front_sliced deals them): 32 / ceil(tiles / 8) slices, of
+// at least kFrontSliceKTiles K tiles each, at most kMaxFrontPlanes.
+// Row stride (floats) of the fp32 front planes (FwdArgs::raw): r3 z columns, then
+// E logits, padded to a multiple of 4 so that every row starts 16-byte aligned
+// (the plane writers store and the epilogue loads z columns 16 bytes at a time).
+constexpr int64_t raw_stride(int64_t r3, int64_t E) { return r3 + (E + 3) / 4 * 4; }
 constexpr int64_t kFrontMinKTiles = 16;
-// K tiles per slice at least: 4 measured no faster at T = 512-4096 (d_in = 1536) and
-// puts T = 3072 into two rounds of work-groups (6 slices x 48 tiles)
-constexpr int64_t kFrontSliceKTiles = 8;
+constexpr int64_t kFrontSliceKTiles = 3;
 constexpr int kMaxFrontPlanes = 8;
+constexpr int64_t kFrontXcds = 8, kFrontGroupsPerXcd = 32;
 inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
   // E_pad = 256 measured slower sliced (C4: front 44.6 us against 34.8 us for the
   // split z / router front plus 7.7 us of k_expand_cz)
@@ -149,10 +156,14 @@ inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
   // measured at d_in = 1536: slices win up to 64 tiles (T = 4096); at 128 tiles
   // the 32-token front is faster
   if (4 * tiles > 256 || nkt < kFrontMinKTiles) return 1;
-  int64_t s = (256 + tiles - 1) / tiles;
+  int64_t s = kFrontGroupsPerXcd / ((tiles + kFrontXcds - 1) / kFrontXcds);
   if (s > nkt / kFrontSliceKTiles) s = nkt / kFrontSliceKTiles;
   if (s > kMaxFrontPlanes) s = kMaxFrontPlanes;
   return s > 1 ? (int)s : 1;
+}
+// signal flags of k_front_sliced: one per (64-token tile, slice)
+inline int64_t front_sliced_flags(int64_t T, int split) {
+  return split > 1 ? (T + 63) / 64 * split : 0;
 }
 
 // Output tiles (256 tokens x 64 channels) of the grouped core and the split S of
@@ -234,6 +245,11 @@ hipError_t launch_expand_cz(const FwdArgs& a, hipStream_t stream);
 // itself (a.cz): the single-kind front (not the K-sliced one nor the split one of
 // the widest routers) with at most 32 ranks. Then no launch_expand_cz is needed.
 bool front_fuses_cz(const FwdArgs& a, hipStream_t stream);
+// The K-sliced front's slices and per-token epilogue in one launch (k_front_sliced):
+// bf16, front_split > 1, the workspace's signal words, a device of 256 compute units
+// (8 XCDs of 32), and the stream not being captured (its flags have several
+// consumers and stay set). Same arithmetic as the two-launch path.
+bool front_sliced_ok(const FwdArgs& a, hipStream_t stream);
 // Folded bf16 plans (r1 = 4, r3 = 256, K = 1024, E_pad = 256) whose large-T
 // out-projection is k_outproj_wide: it forms c (x) z in its loop from the z and c
 // the front stores.

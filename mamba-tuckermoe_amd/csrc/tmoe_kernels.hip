@@ -9,6 +9,7 @@
 #include "tmoe_outproj_mid.hpp"
 #include "tmoe_front_ks.hpp"
 #include "tmoe_fused.hpp"
+#include "tmoe_front_sliced.hpp"
 
 namespace tmoe {
 namespace {
@@ -44,17 +45,26 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
   if constexpr (std::is_same<Elt, EltBF16>::value) {
     if (a.front_split > 1) {
       // K slices of 64-token tiles (k_front_part), then the per-token epilogue over
-      // their planes
+      // their planes: in one launch (k_front_sliced, a fresh epoch for its signals)
+      // or two
       constexpr int kStageBytes = (kFrontBM + R3 + 32 * NR) * 128;
       constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
-      const int64_t stride = a.T * (a.r3 + a.E);
+      if (a.front_one) {
+        FwdArgs b = a;
+        b.epoch = next_epoch();
+        hipLaunchKernelGGL(
+            (dev::k_front_sliced<Elt, R3, NR, kFrontPFA, kFrontBM, NS, kFrontWM>),
+            dim3(dev::sliced::kGrid), dim3(64 * NW * kFrontWM), 0, st, b, b.raw, b.front_split);
+        return hipGetLastError();
+      }
+      const int64_t stride = a.T * raw_stride(a.r3, a.E);
       hipLaunchKernelGGL((dev::k_front_part<Elt, R3, NR, kFrontPFA, kFrontBM, NS, kFrontWM>),
                          dim3(cdiv(a.T, kFrontBM), a.front_split), dim3(64 * NW * kFrontWM), 0,
                          st, a, a.raw, a.front_split);
       if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-      hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256),
-                         (size_t)(a.E * a.r1) * sizeof(float), st, a,
-                         (const float*)a.raw, a.front_split, stride);
+      hipLaunchKernelGGL((dev::k_front_epi<Elt, R3 / 64, kMaxFrontPlanes, 2>),
+                         dim3(cdiv(a.T, 4)), dim3(256), (size_t)(a.E * a.r1) * sizeof(float), st,
+                         a, (const float*)a.raw, a.front_split, stride);
       return hipGetLastError();
     }
   }
@@ -287,9 +297,15 @@ hipError_t launch_small_front_t(const FwdArgs& a, hipStream_t st) {
   const dim3 grid(cdiv(a.r3 + a.E, 16), cdiv(a.T, 16 * MF)), block(64 * kSkW);
   hipLaunchKernelGGL((dev::k_sk_front<Elt, MF, kSkW>), grid, block, 0, st, a, a.raw);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  hipLaunchKernelGGL(dev::k_front_epi<Elt>, dim3(cdiv(a.T, 4)), dim3(256),
-                     (size_t)(a.E * a.r1) * sizeof(float), st, a,
-                     (const float*)a.raw, 1, (int64_t)0);
+  const dim3 eg(cdiv(a.T, 4)), eb(256);
+  const size_t ue_bytes = (size_t)(a.E * a.r1) * sizeof(float);
+  const float* raw = a.raw;
+  if (a.r3 == 256)
+    hipLaunchKernelGGL((dev::k_front_epi<Elt, 4, 1, 4>), eg, eb, ue_bytes, st, a, raw, 1, (int64_t)0);
+  else if (a.r3 == 128)
+    hipLaunchKernelGGL((dev::k_front_epi<Elt, 2, 1, 4>), eg, eb, ue_bytes, st, a, raw, 1, (int64_t)0);
+  else
+    hipLaunchKernelGGL((dev::k_front_epi<Elt, 1, 1, 4>), eg, eb, ue_bytes, st, a, raw, 1, (int64_t)0);
   return hipGetLastError();
 }
 
@@ -565,6 +581,15 @@ bool front_fuses_cz(const FwdArgs& a, hipStream_t st) {
   // k_expand_cz instead)
   if (a.r3 == 256 && a.E_pad == 256) return a.r1 <= 32 && a.sync != nullptr && !stream_capturing(st);
   return a.r1 <= 32;
+}
+
+bool front_sliced_ok(const FwdArgs& a, hipStream_t st) {
+  if (a.dtype != kDtypeBF16 || a.front_split <= 1 || !a.sync || a.E_pad > 128) return false;
+  // every (XCD, slot) pair of the grid holds at most one slice
+  const int64_t per_xcd = ((int64_t)cdiv(a.T, kFrontBM) + dev::sliced::kXcds - 1) /
+                          dev::sliced::kXcds;
+  return per_xcd * a.front_split <= dev::sliced::kGroupsPerXcd &&
+         cu_count() == dev::sliced::kGrid && !stream_capturing(st);
 }
 
 uint32_t next_epoch() {

@@ -1453,9 +1453,14 @@ __device__ __forceinline__ void front_part_tile(const FwdArgs& a, float* __restr
   rx.init(wn, lane, BM + R3);
   gemm_mainloop<TL, Elt>(acc, al, bl, kt1 - kt0, smem, rx);
 
-  const int W = R3 + (int)a.E;
+  const int W = (int)raw_stride(R3, a.E);
   float* plane = raw + (int64_t)sl * a.T * W + m0 * W;
-  // z columns straight from the accumulators: a half-wave writes 128 contiguous bytes
+  // z columns through LDS (rows of R3 + 4 floats), then out as 16-byte row chunks
+  // (the accumulators give a lane one column of 16 rows: 4-byte stores)
+  constexpr int ZL = R3 + 4;
+  static_assert(BM * ZL * 4 <= G::kSmemBytes, "the z tile fits the LDS");
+  float* zt = reinterpret_cast<float*>(smem);
+  __syncthreads();   // the main loop's last LDS reads are done
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1463,9 +1468,14 @@ __device__ __forceinline__ void front_part_tile(const FwdArgs& a, float* __restr
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = wrow + i * 32 + acc_row(lane, e);
-        if (row < rows_valid)
-          plane[(int64_t)row * W + wn * TL::kWaveN + j * 32 + (lane & 31)] = acc[i][j][e];
+        zt[row * ZL + wn * TL::kWaveN + j * 32 + (lane & 31)] = acc[i][j][e];
       }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < rows_valid * (R3 / 4); idx += TL::kThreads) {
+    const int row = idx / (R3 / 4), c4 = idx - row * (R3 / 4);
+    *reinterpret_cast<float4*>(plane + (int64_t)row * W + 4 * c4) =
+        *reinterpret_cast<const float4*>(zt + row * ZL + 4 * c4);
+  }
   // router columns: through LDS (split-K router: one partial plane per wave, added
   // in wave order), the first E of them
   __syncthreads();

@@ -207,13 +207,14 @@ struct SkLds {
   static constexpr int kFloats = MF * 256 + W * MF * 256;
 };
 
-// raw (T, r3 + E) fp32 = x [U_in | W_r^T] (the router rows past E are not computed)
+// raw (T, r3 + E) fp32 = x [U_in | W_r^T] (the router rows past E are not computed),
+// rows raw_stride(r3, E) floats apart
 template <class Elt, int MF, int W>
 __global__ __launch_bounds__(64 * W) void k_sk_front(FwdArgs a, float* raw) {
   typedef typename Elt::T T;
   __shared__ float red[SkLds<MF, W>::kFloats];
   const int64_t n0 = (int64_t)blockIdx.x * 16, m0 = (int64_t)blockIdx.y * MF * 16;
-  const int64_t N = a.r3 + a.E;
+  const int64_t N = a.r3 + a.E, RS = raw_stride(a.r3, a.E);
   const int rows_valid = (int)(a.T - m0 < MF * 16 ? a.T - m0 : MF * 16);
   const int cols_valid = (int)(N - n0 < 16 ? N - n0 : 16);
   const int64_t rb = a.d_in * (int64_t)sizeof(T);
@@ -222,51 +223,94 @@ __global__ __launch_bounds__(64 * W) void k_sk_front(FwdArgs a, float* raw) {
                              cols_valid, a.d_in, red);
   for (int e = threadIdx.x; e < MF * 256; e += 64 * W) {
     const int row = e >> 4, c = e & 15;
-    if (row < rows_valid && c < cols_valid) raw[(m0 + row) * N + n0 + c] = red[e];
+    if (row < rows_valid && c < cols_valid) raw[(m0 + row) * RS + n0 + c] = red[e];
   }
 }
 
 // The per-token front epilogue, one wave per token: z = RMSNorm(raw z (* U_in
 // scales)) * gain; logits; top-k (rank_key order: larger first, NaN above
 // numbers, lower index on ties); softmax over the selected; c = sum_j w_j
-// U_expert[e_j]. epi_load issues a token's loads (the lane's z columns lane + 64 q
-// and logits lane + 64 q of every raw plane, added in plane order; gain and
-// U_in scales); epi_finish computes and writes the results.
+// U_expert[e_j]. Lane l holds the z columns G l .. G l + G - 1 (G = r3 / 64: one
+// 4-, 8- or 16-byte load per raw plane) and the logits l + 64 q (q < LQ, E <= 64
+// LQ). epi_load issues a token's loads (every raw plane, added in plane order;
+// gain and U_in scales) with no branch between them, so that they are all in
+// flight at once; epi_finish computes and writes the results.
 struct EpiLoad {
-  float zr[4], lr[4], gv[4], zs[4];
+  float zr[4], lr[4], gv[4], zs[4];   // z, gain, U_in scale: [q] = column G l + q
 };
 
+// G consecutive floats at p into v[0 .. G-1] (p aligned to 4 G bytes)
+template <int G>
+__device__ __forceinline__ void load_cols(const float* p, float (&v)[4]) {
+  if constexpr (G == 4) {
+    const float4 u = *reinterpret_cast<const float4*>(p);
+    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+  } else if constexpr (G == 2) {
+    const float2 u = *reinterpret_cast<const float2*>(p);
+    v[0] = u.x; v[1] = u.y;
+  } else {
+    v[0] = p[0];
+  }
+}
+
+typedef uint32_t u32x2e __attribute__((ext_vector_type(2)));
+
+// v[0 .. G-1] as G consecutive elements at p (aligned to G elements)
+template <int G>
+__device__ __forceinline__ void store_cols(uint16_t* p, const float (&v)[4]) {
+  if constexpr (G == 4) {
+    u32x2e u;
+    u.x = pack_bf16x2(v[0], v[1]);
+    u.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<u32x2e*>(p) = u;
+  } else if constexpr (G == 2) {
+    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(v[0], v[1]);
+  } else {
+    *p = f32_to_bf16_bits(v[0]);
+  }
+}
+template <int G>
+__device__ __forceinline__ void store_cols(float* p, const float (&v)[4]) {
+  if constexpr (G == 4) *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  else if constexpr (G == 2) *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  else p[0] = v[0];
+}
+
+// nplanes (1 .. KP) raw planes, plane_stride floats apart. KP planes are loaded:
+// those past nplanes load the last plane again (in bounds) and are not added.
+// Logit loads past E read logit E - 1 (in bounds) and are not added.
+template <int G, int KP, int LQ>
 __device__ __forceinline__ void epi_load(const FwdArgs& a, const float* raw, int nplanes,
                                          int64_t plane_stride, int64_t t, int lane, EpiLoad& L) {
-  const int R3 = (int)a.r3, E = (int)a.E;
+  constexpr int R3 = 64 * G;
+  const int E = (int)a.E;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     L.zr[q] = 0.f; L.lr[q] = 0.f; L.gv[q] = 0.f; L.zs[q] = 1.f;
-    const int j = lane + 64 * q;
-    if (j < R3) {
-      L.gv[q] = a.gain[j];
-      if (a.zscale) L.zs[q] = a.zscale[j];
+  }
+  load_cols<G>(a.gain + G * lane, L.gv);
+  if (a.zscale) load_cols<G>(a.zscale + G * lane, L.zs);
+  const float* row = raw + t * raw_stride(R3, E);
+  float zp[KP][4], lp[KP][LQ];
+#pragma unroll
+  for (int p = 0; p < KP; ++p) {
+    const float* pr = row + (p < nplanes ? p : nplanes - 1) * plane_stride;
+    load_cols<G>(pr + G * lane, zp[p]);
+#pragma unroll
+    for (int q = 0; q < LQ; ++q) {
+      const int e = lane + 64 * q;
+      lp[p][q] = pr[R3 + (e < E ? e : E - 1)];
     }
   }
-  const float* row = raw + t * (R3 + E);
-  float zp[kMaxFrontPlanes][4], lp[kMaxFrontPlanes][4];
 #pragma unroll
-  for (int p = 0; p < kMaxFrontPlanes; ++p)
-    if (p < nplanes)
+  for (int p = 0; p < KP; ++p) {
+    const bool on = p < nplanes;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int j = lane + 64 * q;
-        zp[p][q] = j < R3 ? row[p * plane_stride + j] : 0.f;
-        lp[p][q] = j < E ? row[p * plane_stride + R3 + j] : 0.f;
-      }
+    for (int q = 0; q < G; ++q) L.zr[q] = on ? L.zr[q] + zp[p][q] : L.zr[q];
 #pragma unroll
-  for (int p = 0; p < kMaxFrontPlanes; ++p)
-    if (p < nplanes)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        L.zr[q] += zp[p][q];
-        L.lr[q] += lp[p][q];
-      }
+    for (int q = 0; q < LQ; ++q)
+      L.lr[q] = on && lane + 64 * q < E ? L.lr[q] + lp[p][q] : L.lr[q];
+  }
 }
 
 // Token t's results from its loads L (every lane of the wave calls it). ue:
@@ -274,19 +318,19 @@ __device__ __forceinline__ void epi_load(const FwdArgs& a, const float* raw, int
 // outputs; z_global: write z (or, when a.cz is set, the Khatri-Rao row c (x) z)
 // to a's buffers; z_row / c_row (LDS, or null): the token's z as stored (r3
 // elements) and c (r1 floats).
-template <class Elt>
+template <class Elt, int G>
 __device__ __forceinline__ void epi_finish(const FwdArgs& a, int64_t t, int lane, const EpiLoad& L,
                                            const float* ue, bool routing, bool z_global,
                                            typename Elt::T* z_row, float* c_row) {
   typedef typename Elt::T T;
-  const int R3 = (int)a.r3, E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
+  constexpr int R3 = 64 * G;
+  const int E = (int)a.E, K = (int)a.k, R1 = (int)a.r1;
   float zv[4];
   float ss = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int j = lane + 64 * q;
     float v = 0.f;
-    if (j < R3) {
+    if (q < G) {
       v = L.zr[q];
       if (a.zscale) v *= L.zs[q];
     }
@@ -296,14 +340,9 @@ __device__ __forceinline__ void epi_finish(const FwdArgs& a, int64_t t, int lane
   ss = wave_sum(ss);
   const float inv_rms = 1.f / sqrtf(ss / (float)R3 + a.eps);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int j = lane + 64 * q;
-    zv[q] = round_as((zv[q] * inv_rms) * L.gv[q], Elt{});   // z as stored
-    if (j < R3) {
-      if (z_global && !a.cz) store_from_f32(reinterpret_cast<T*>(a.z) + t * R3 + j, zv[q]);
-      if (z_row) store_from_f32(z_row + j, zv[q]);
-    }
-  }
+  for (int q = 0; q < 4; ++q) zv[q] = round_as((zv[q] * inv_rms) * L.gv[q], Elt{});   // z as stored
+  if (z_global && !a.cz) store_cols<G>(reinterpret_cast<T*>(a.z) + t * R3 + G * lane, zv);
+  if (z_row) store_cols<G>(z_row + G * lane, zv);
   uint64_t key[4];   // rank_key order; 0 past E and once taken
   float sv[4];       // the ranked scores (router_mode 1: capped ones)
   const int mode = a.router_mode;
@@ -368,23 +407,22 @@ __device__ __forceinline__ void epi_finish(const FwdArgs& a, int64_t t, int lane
     if (c_row) c_row[lane] = cr;
   }
   if (z_global && a.cz) {   // folded plans: the Khatri-Rao row c (x) z in place of z
-    T* dst = static_cast<T*>(a.cz) + t * R1 * R3;
+    T* dst = static_cast<T*>(a.cz) + t * R1 * R3 + G * lane;
 #pragma unroll 1
     for (int r = 0; r < R1; ++r) {
       const float c_r = lane_value(cr, r);
+      float v[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int j = lane + 64 * q;
-        if (j < R3) store_from_f32(dst + r * R3 + j, c_r * zv[q]);
-      }
+      for (int q = 0; q < 4; ++q) v[q] = c_r * zv[q];
+      store_cols<G>(dst + r * R3, v);
     }
   }
 }
 
-// The front epilogue as a kernel, one wave per token. raw: nplanes (<=
-// kMaxFrontPlanes) planes of T rows (plane_stride floats apart), added in plane
-// order (the large-T front in K slices; the small-T front writes one).
-template <class Elt>
+// The front epilogue as a kernel, one wave per token. raw: nplanes (<= KP)
+// planes of T rows (plane_stride floats apart), added in plane order (the large-T
+// front in K slices; the small-T front writes one). G = r3 / 64, E <= 64 LQ.
+template <class Elt, int G, int KP, int LQ>
 __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, int nplanes,
                                                    int64_t plane_stride) {
   // U_expert (E x r1 floats: the launch's dynamic LDS) is staged while the rows load
@@ -394,11 +432,11 @@ __global__ __launch_bounds__(256) void k_front_epi(FwdArgs a, const float* raw, 
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool live = t < a.T;   // whole waves
   EpiLoad L;
-  if (live) epi_load(a, raw, nplanes, plane_stride, t, lane, L);
+  if (live) epi_load<G, KP, LQ>(a, raw, nplanes, plane_stride, t, lane, L);
   for (int i = threadIdx.x; i < E * R1; i += 256) ue[i] = a.uexp[i];
   __syncthreads();
   if (!live) return;   // no barriers below
-  epi_finish<Elt>(a, t, lane, L, ue, true, true, nullptr, nullptr);
+  epi_finish<Elt, G>(a, t, lane, L, ue, true, true, nullptr, nullptr);
 }
 
 // The Khatri-Rao A operand from z and c rows staged in LDS (SkKhatriRao's
@@ -444,6 +482,32 @@ inline size_t sk_epi_dyn_bytes(int mf, const FwdArgs& a) {
   return (size_t)mf * 16 * zs * es + (size_t)mf * 16 * a.r1 * 4 + (size_t)a.E * a.r1 * 4;
 }
 
+// k_sk_epi_gemm's epilogue of its MF 16 tokens (TPW per wave, W waves) into LDS
+// (z rows zl, ZS elements apart; c rows cl), with U_expert staged into ue: every
+// token's loads first, then the results. Ends with a barrier.
+template <class Elt, int G, int TPW, int W>
+__device__ __forceinline__ void sk_epi_tokens(const FwdArgs& a, int64_t m0, int rows_valid,
+                                              bool routing, float* ue, typename Elt::T* zl,
+                                              int ZS, float* cl) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int E = (int)a.E, R1 = (int)a.r1;
+  EpiLoad L[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int row = wave + W * i;
+    if (row < rows_valid) epi_load<G, 1, 4>(a, a.raw, 1, 0, m0 + row, lane, L[i]);
+  }
+  for (int i = threadIdx.x; i < E * R1; i += 64 * W) ue[i] = a.uexp[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int row = wave + W * i;
+    if (row < rows_valid)
+      epi_finish<Elt, G>(a, m0 + row, lane, L[i], ue, routing, false, zl + row * ZS,
+                         cl + row * R1);
+  }
+}
+
 // The front epilogue fused into the Khatri-Rao GEMM that follows it (small T, raw
 // from k_sk_front in one plane): every work-group runs the epilogue of its MF 16
 // tokens into LDS (the token loads are issued first, for every token of a wave),
@@ -475,21 +539,10 @@ __global__ __launch_bounds__(64 * W) void k_sk_epi_gemm(FwdArgs a) {
   const char* bsrc = reinterpret_cast<const char*>(kCore ? a.coreT : a.uoutT) + n0 * rb;
   u32x4 bpre[1][2];
   skinny_b_first<Elt, W, 1>(bsrc, rb, cols_valid, K, bpre);
-  EpiLoad L[TPW];
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int row = wave + W * i;
-    if (row < rows_valid) epi_load(a, a.raw, 1, 0, m0 + row, lane, L[i]);
-  }
-  for (int i = threadIdx.x; i < E * R1; i += 64 * W) ue[i] = a.uexp[i];
-  __syncthreads();
   const bool routing = blockIdx.x == 0;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int row = wave + W * i;
-    if (row < rows_valid)
-      epi_finish<Elt>(a, m0 + row, lane, L[i], ue, routing, false, zl + row * ZS, cl + row * R1);
-  }
+  if (R3 == 256) sk_epi_tokens<Elt, 4, TPW, W>(a, m0, rows_valid, routing, ue, zl, ZS, cl);
+  else if (R3 == 128) sk_epi_tokens<Elt, 2, TPW, W>(a, m0, rows_valid, routing, ue, zl, ZS, cl);
+  else sk_epi_tokens<Elt, 1, TPW, W>(a, m0, rows_valid, routing, ue, zl, ZS, cl);
   __syncthreads();
   SkKhatriRaoLds<Elt> as{zl, cl, R1, R3, rows_valid};
   if constexpr (kCore) {

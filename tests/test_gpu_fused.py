@@ -1,5 +1,5 @@
-"""The one-launch large-T forward (k_fused_large) and the reporting of lost
-in-launch signals.
+"""The one-launch large-T forward (k_fused_large), the one-launch K-sliced mid-T
+front (k_front_sliced) and the reporting of lost in-launch signals.
 
 The large-T forward of a folded bf16 plan (r3 = 256, E <= 32, d_out % 288 == 0,
 T >= 8192 at the C3 shapes) runs front and out-projection in one persistent grid
@@ -110,9 +110,80 @@ def test_fused_workspace_reuse_and_graph(pkg, dev):
     m.check_signals()
 
 
+@pytest.mark.parametrize("T", [300, 777, 2048, 3001, 4096])
+def test_sliced_front_matches_two_launches(pkg, dev, T):
+    """The K-sliced mid-T front in one launch (k_front_sliced: slices, then the
+    per-token epilogue once a tile's slices are in) against the same slices in two
+    launches (TMOE_FLAG_NO_FUSE: k_front_part + k_front_epi): bit-identical outputs
+    and routing, a clean status block, and the float64 oracle."""
+    w = pkg.WORKLOADS["C3"]
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, T, stream=19)
+    xd = x.to(dev)
+    m = _module(pkg, dev, w, params)
+    out, idx, wts = _forward(m, xd)
+    m.check_signals()
+    m2 = _module(pkg, dev, w, params, fuse=False)
+    out2, idx2, wts2 = _forward(m2, xd)
+    assert torch.equal(out, out2) and torch.equal(idx, idx2) and torch.equal(wts, wts2)
+    ref = onp.forward_f64(x, params, w.k)
+    err = onp.rel_l2(out.float().cpu().numpy(), ref["out"])
+    mism = int((idx.cpu().numpy() != ref["idx"]).any(1).sum())
+    print(f"sliced front T={T}: rel_l2(out, f64)={err:.3e} routing_mismatch_rows={mism}",
+          flush=True)
+    assert mism == 0 and err <= 1e-2
+
+
+def test_sliced_front_workspace_reuse_and_graph(pkg, dev):
+    """The one-launch sliced front does not depend on what the workspace held (0xFF
+    bytes, random bytes, the flags of the previous forward); a captured forward
+    (the two-launch sliced front) replays to the same bits, with eager forwards
+    between the replays."""
+    w = pkg.WORKLOADS["C3"]
+    T = 2048
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w, T, stream=23).to(dev)
+    m = _module(pkg, dev, w, params)
+    plan, packed = m.plan(), m.packed()
+    L = pkg._lib.lib()
+    with torch.no_grad():
+        ref = m(x)
+    torch.cuda.synchronize()
+    ws_bytes = plan.workspace_bytes(T)
+    g = torch.Generator(device=dev).manual_seed(7)
+    fills = [torch.full((ws_bytes,), 255, dtype=torch.uint8, device=dev),
+             torch.randint(0, 256, (ws_bytes,), dtype=torch.uint8, device=dev, generator=g)]
+    for ws in fills:
+        for _ in range(2):
+            out = torch.empty_like(ref)
+            pkg._lib.check(L.tmoe_forward(plan.ptr, x.data_ptr(), T, packed.data_ptr(),
+                                          out.data_ptr(), None, None, None, ws.data_ptr(),
+                                          ws_bytes, torch.cuda.current_stream().cuda_stream))
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+    m.check_signals()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out_g = torch.empty_like(ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph, stream=s):
+        m.forward_raw(x, out=out_g)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref)
+        with torch.no_grad():
+            assert torch.equal(m(x), ref)
+        torch.cuda.synchronize()
+    m.check_signals()
+
+
 # workloads whose forward signals between work-groups of one launch: the
-# one-launch large-T forward (C3), the E = 256 front (C4) and the decode launch (C2)
-@pytest.mark.parametrize("name,T", [("C3", 16384), ("C4", 600), ("C2", 32)])
+# one-launch large-T forward (C3), the one-launch sliced front (C3 at T = 2048),
+# the E = 256 front (C4) and the decode launch (C2)
+@pytest.mark.parametrize("name,T", [("C3", 16384), ("C3", 2048), ("C4", 600), ("C2", 32)])
 def test_lost_signal_is_reported(pkg, dev, name, T):
     """With a wait budget of 0 polls every in-launch wait gives up at once; the
     kernels still complete, the status block records it, and the module raises
