@@ -542,8 +542,10 @@ def measure(pkg, w, args, *, steps, warmup, rotate_mb, no_fold, no_fuse, cpu, la
     kr = path == pkg._lib.TMOE_PATH_LARGE_KR
     sb = (w.stage_bytes_kr(T, rk) if kr else
           w.stage_bytes_folded(T, rk) if folded else w.stage_bytes())
-    one_launch = path in (pkg._lib.TMOE_PATH_DECODE, pkg._lib.TMOE_PATH_FUSED)
-    kname = {pkg._lib.TMOE_PATH_DECODE: "k_sk_decode", pkg._lib.TMOE_PATH_FUSED: "k_fused_large"}
+    one_launch = path in (pkg._lib.TMOE_PATH_DECODE, pkg._lib.TMOE_PATH_FUSED,
+                          pkg._lib.TMOE_PATH_FUSED_MID)
+    kname = {pkg._lib.TMOE_PATH_DECODE: "k_sk_decode", pkg._lib.TMOE_PATH_FUSED: "k_fused_large",
+             pkg._lib.TMOE_PATH_FUSED_MID: "k_fused_mid"}
     if one_launch:
         # the one kernel (recorded as the front stage) runs the whole layer; the other
         # two stages record no kernel
@@ -577,7 +579,8 @@ def measure(pkg, w, args, *, steps, warmup, rotate_mb, no_fold, no_fuse, cpu, la
         log(f"[{label}] copy calibration: 3 x {args.copy_calibration_mib} MiB device copies")
 
     full_size = T == pkg.WORKLOADS[w.name].T
-    stage_key = dom + ("_fused" if path == pkg._lib.TMOE_PATH_FUSED else
+    stage_key = dom + ("_fused" if path in (pkg._lib.TMOE_PATH_FUSED,
+                                            pkg._lib.TMOE_PATH_FUSED_MID) else
                        "_kr" if kr else "_folded" if folded else "")
     traffic = traffic_per_launch(w.name, stage_key) if full_size else None
     # MFMA-busy share of the dominant stage from the committed counter pass (the

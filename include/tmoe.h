@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMOE_ABI_VERSION 11
+#define TMOE_ABI_VERSION 12
 
 /* error codes */
 #define TMOE_OK            0
@@ -255,6 +255,9 @@ int tmoe_forward_static(const tmoe_plan* plan, const void* x, int64_t T, const v
 #define TMOE_PATH_FUSED  4  /* large T, folded: the whole layer in one launch         */
 #define TMOE_PATH_LARGE_KR 5 /* large T, folded, E > 128: front (stores z and c) and an
                                out-projection that forms c (x) z in its loop            */
+#define TMOE_PATH_FUSED_MID 6 /* mid T (256 < T <= 2048 at d_out = 2304), folded, r3 = 256,
+                                E <= 32: the whole layer in one launch (K-sliced front and
+                                128 x 144 out-projection tiles)                          */
 int tmoe_forward_path(const tmoe_plan* plan, int64_t T);
 
 /* Lost in-launch signals. No counterpart in the reference (its forward has no

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before libtmoe.so)
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmoe.so")
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 TMOE_OK, TMOE_EINVAL, TMOE_EUNSUPPORTED, TMOE_EHIP, TMOE_ESIGNAL = 0, -1, -2, -3, -4
 TMOE_F32, TMOE_BF16, TMOE_BF16_FP8W = 0, 1, 2
 TMOE_ROUTER_SOFTMAX_TOPK, TMOE_ROUTER_CAPPED = 0, 1
@@ -29,9 +29,11 @@ TMOE_FLAG_NO_FUSE = 2
 TMOE_STATUS_SIGNAL = 1
 TMOE_PATH_SMALL, TMOE_PATH_DECODE, TMOE_PATH_LARGE, TMOE_PATH_FUSED = 1, 2, 3, 4
 TMOE_PATH_LARGE_KR = 5
+TMOE_PATH_FUSED_MID = 6
 PATH_NAMES = {1: "small-T kernels", 2: "one launch (k_sk_decode)",
               3: "front + out-projection launches", 4: "one launch (k_fused_large)",
-              5: "front (z, c) + out-projection forming c (x) z (k_outproj_wide_kr)"}
+              5: "front (z, c) + out-projection forming c (x) z (k_outproj_wide_kr)",
+              6: "one launch (k_fused_mid)"}
 TMOE_LATENT_P_F32 = 0x100   # or'ed into a latent call's dtype: p and dp are fp32
 N_STAGES = 3
 STAGE_NAMES = ("front", "core", "out_proj")

@@ -592,11 +592,14 @@ int forward_impl(const tmoe_plan* p, const void* x, int64_t T, const void* packe
   a.front_one = !(p->s.flags & TMOE_FLAG_NO_FUSE) && tmoe::front_sliced_ok(a, st);
   if (fold) a = folded_args(p, a, packed, st);
   // the large-T folded forward in one launch where the plan, T and the device allow
-  const bool fused = fold && !small && !(p->s.flags & TMOE_FLAG_NO_FUSE) &&
-                     tmoe::fused_large_ok(a, st);
-  const Launch big_path[kStages] = {fused ? tmoe::launch_fused_large : tmoe::launch_front,
-                                    fused ? launch_nothing : fold ? launch_cz : tmoe::launch_core,
-                                    fused ? launch_nothing : tmoe::launch_outproj};
+  const bool fuse_ok = fold && !small && !(p->s.flags & TMOE_FLAG_NO_FUSE);
+  const bool fused = fuse_ok && tmoe::fused_large_ok(a, st);
+  // the mid-T folded forward in one launch (K-sliced front + 128 x 144 tiles)
+  const bool fused_mid = fuse_ok && !fused && tmoe::fused_mid_ok(a, st);
+  const Launch big_path[kStages] = {
+      fused ? tmoe::launch_fused_large : fused_mid ? tmoe::launch_fused_mid : tmoe::launch_front,
+      fused || fused_mid ? launch_nothing : fold ? launch_cz : tmoe::launch_core,
+      fused || fused_mid ? launch_nothing : tmoe::launch_outproj};
   // folded: the out-projection builds c (x) z from z and c itself (no core stage)
   Launch small_path[kStages];
   small_stages(a, fold, st, small_path);
@@ -837,6 +840,8 @@ int tmoe_forward_path(const tmoe_plan* p, int64_t T) {
   if (p->fold) {
     const tmoe::FwdArgs f = folded_args(p, a, fake, nullptr);
     if (!(p->s.flags & TMOE_FLAG_NO_FUSE) && tmoe::fused_large_shape_ok(f)) return TMOE_PATH_FUSED;
+    if (!(p->s.flags & TMOE_FLAG_NO_FUSE) && tmoe::fused_mid_shape_ok(f))
+      return TMOE_PATH_FUSED_MID;
     if (f.kr) return TMOE_PATH_LARGE_KR;
   }
   return TMOE_PATH_LARGE;

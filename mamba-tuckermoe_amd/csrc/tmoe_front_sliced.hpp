@@ -40,22 +40,17 @@ constexpr int kGroupsPerXcd = 32;   // compute units per XCD: one work-group eac
 constexpr int kGrid = kXcds * kGroupsPerXcd;
 }  // namespace sliced
 
-// raw: S planes of T rows of raw_stride(r3, E) floats; the flags
-// of tile ft are sync_flag(ft S) .. sync_flag(ft S + S - 1).
+// Slice sl of front tile ft, then the epilogue of its share of the tile's tokens:
+// k_front_sliced's work for one (tile, slice), by all the work-group's threads.
+// raw: S planes of T rows of raw_stride(r3, E) floats; the flags of tile ft are
+// sync_flag(ft S) .. sync_flag(ft S + S - 1). smem: FrontPartGeom::kSmemBytes.
 template <class Elt, int R3, int NR, int PFA, int BM, int NS, int WMF>
-__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front_sliced(
-    FwdArgs a, float* __restrict__ raw, int S) {
+__device__ __forceinline__ void front_slice_work(const FwdArgs& a, float* __restrict__ raw,
+                                                 int S, int ft, int sl, u32x4* smem) {
   typedef FrontPartGeom<Elt, R3, NR, PFA, BM, NS, WMF> G;
   constexpr int kThreads = 64 * G::NWT;
   // U_expert: E <= E_pad <= 128 experts (the K-sliced front's routers), r1 <= 64
   static_assert(G::kSmemBytes >= 16 + 4 * 64 * 128, "U_expert fits the LDS");
-  __shared__ u32x4 smem[G::kSmemBytes / 16];
-  const int x = xcc_id(), i = (int)blockIdx.x / sliced::kXcds;
-  const int n_ft = (int)((a.T + BM - 1) / BM);
-  const int nfx = (n_ft - x + sliced::kXcds - 1) / sliced::kXcds;   // tiles x, x + 8, ...
-  if (i >= nfx * S) return;   // no slice for this work-group
-  const int ft = x + sliced::kXcds * (i / S), sl = i % S;
-
   front_part_tile<Elt, R3, NR, PFA, BM, NS, WMF>(a, raw, S, ft, sl, smem);
   sync_publish(a.sync + sync_flag((int64_t)ft * S + sl), a.epoch);
 
@@ -81,6 +76,19 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
     epi_load<R3 / 64, kMaxFrontPlanes, 2>(a, raw, S, plane_stride, t, lane, L);
     epi_finish<Elt, R3 / 64>(a, t, lane, L, ue, true, true, nullptr, nullptr);
   }
+}
+
+template <class Elt, int R3, int NR, int PFA, int BM, int NS, int WMF>
+__global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_front_sliced(
+    FwdArgs a, float* __restrict__ raw, int S) {
+  typedef FrontPartGeom<Elt, R3, NR, PFA, BM, NS, WMF> G;
+  __shared__ u32x4 smem[G::kSmemBytes / 16];
+  const int x = xcc_id(), i = (int)blockIdx.x / sliced::kXcds;
+  const int n_ft = (int)((a.T + BM - 1) / BM);
+  const int nfx = (n_ft - x + sliced::kXcds - 1) / sliced::kXcds;   // tiles x, x + 8, ...
+  if (i >= nfx * S) return;   // no slice for this work-group
+  front_slice_work<Elt, R3, NR, PFA, BM, NS, WMF>(a, raw, S, x + sliced::kXcds * (i / S), i % S,
+                                                  smem);
 }
 
 }  // namespace dev

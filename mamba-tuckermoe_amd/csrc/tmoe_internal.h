@@ -161,9 +161,10 @@ inline int front_split(int64_t T, int64_t d_in, int64_t E_pad, bool bf16) {
   if (s > kMaxFrontPlanes) s = kMaxFrontPlanes;
   return s > 1 ? (int)s : 1;
 }
-// signal flags of k_front_sliced: one per (64-token tile, slice)
+// signal flags of the K-sliced front in one launch: one per (64-token tile, slice)
+// for the slice, and (k_fused_mid) one more per (tile, slice) for its epilogue
 inline int64_t front_sliced_flags(int64_t T, int split) {
-  return split > 1 ? (T + 63) / 64 * split : 0;
+  return split > 1 ? 2 * ((T + 63) / 64) * split : 0;
 }
 
 // Output tiles (256 tokens x 64 channels) of the grouped core and the split S of
@@ -250,6 +251,13 @@ bool front_fuses_cz(const FwdArgs& a, hipStream_t stream);
 // (8 XCDs of 32), and the stream not being captured (its flags have several
 // consumers and stay set). Same arithmetic as the two-launch path.
 bool front_sliced_ok(const FwdArgs& a, hipStream_t stream);
+// The whole mid-T forward of a folded plan in one launch (k_fused_mid): the K-sliced
+// front (r3 = 256, E_pad = 32) and the 128 x 144 out-projection tiles, at most 32
+// of each kind per XCD, c (x) z handed over inside each XCD's L2; on a device of 256
+// compute units and not under graph capture (f: the folded forward's arguments).
+bool fused_mid_ok(const FwdArgs& f, hipStream_t stream);
+bool fused_mid_shape_ok(const FwdArgs& f);
+hipError_t launch_fused_mid(const FwdArgs& f, hipStream_t stream);
 // Folded bf16 plans (r1 = 4, r3 = 256, K = 1024, E_pad = 256) whose large-T
 // out-projection is k_outproj_wide: it forms c (x) z in its loop from the z and c
 // the front stores.

@@ -10,6 +10,7 @@
 #include "tmoe_front_ks.hpp"
 #include "tmoe_fused.hpp"
 #include "tmoe_front_sliced.hpp"
+#include "tmoe_fused_mid.hpp"
 
 namespace tmoe {
 namespace {
@@ -590,6 +591,37 @@ bool front_sliced_ok(const FwdArgs& a, hipStream_t st) {
                           dev::sliced::kXcds;
   return per_xcd * a.front_split <= dev::sliced::kGroupsPerXcd &&
          cu_count() == dev::sliced::kGrid && !stream_capturing(st);
+}
+
+bool fused_mid_shape_ok(const FwdArgs& a) {
+  if (a.dtype != kDtypeBF16 || !a.cz || a.kr || a.front_split <= 1 || a.r3 != 256 ||
+      a.E_pad != 32 || !a.sync || a.r2 % 64 || !outproj_tiled_ok(a) || !outproj_mid_tiles(a))
+    return false;
+  // per XCD: at most 32 out-projection tiles and 32 front slices
+  const int64_t n_rt = cdiv(a.T, dev::mid::BM);
+  const int64_t nrx = (n_rt + dev::fmid::kXcds - 1) / dev::fmid::kXcds;
+  return nrx * (a.d_out / dev::mid::BN) <= dev::fmid::kGroupsPerXcd &&
+         dev::fmid::kFrontPerRow * nrx * a.front_split <= dev::fmid::kGroupsPerXcd &&
+         cu_count() == dev::fmid::kGrid;
+}
+
+bool fused_mid_ok(const FwdArgs& a, hipStream_t st) {
+  return fused_mid_shape_ok(a) && !stream_capturing(st);
+}
+
+hipError_t launch_fused_mid(const FwdArgs& a, hipStream_t st) {
+  constexpr int R3 = 256, NR = 1;
+  constexpr int kStageBytes = (kFrontBM + R3 + 32 * NR) * 128;
+  constexpr int NS = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
+  constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
+  FwdArgs b = a;
+  b.epoch = next_epoch();
+  hipLaunchKernelGGL(
+      (dev::k_fused_mid<EltBF16, R3, NR, kFrontPFA, kFrontBM, NS, kFrontWM>),
+      dim3(dev::fmid::kGrid), dim3(64 * NW * kFrontWM), 0, st, b, b.raw, b.front_split,
+      static_cast<const uint16_t*>(a.cz), static_cast<const uint16_t*>(a.uoutT),
+      static_cast<uint16_t*>(a.out), a.bias);
+  return hipGetLastError();
 }
 
 uint32_t next_epoch() {

@@ -75,22 +75,19 @@ __device__ __forceinline__ void mid_step(f32x4m (&acc)[mid::FM][mid::FN],
     }
 }
 
-// A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32.
-__global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict__ A,
-                                                     const uint16_t* __restrict__ Bt,
-                                                     uint16_t* __restrict__ C,
-                                                     const float* __restrict__ bias, int M,
-                                                     int N, int K) {
+// Output tile (tm, tn) of out = A Bt^T + bias, by the work-group's threads 0 ..
+// 255 (waves 0-3; no other wave may be alive at its barriers). A (M rows, K), Bt
+// (N rows, K), C (M, N) bf16 bits; bias (N) fp32; smem: NS kStage 16-byte slots.
+__device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
+                                                 const uint16_t* __restrict__ Bt,
+                                                 uint16_t* __restrict__ C,
+                                                 const float* __restrict__ bias, int M, int N,
+                                                 int K, int tm, int tn, u32x4* smem) {
   using namespace mid;
-  __shared__ u32x4 smem[NS * kStage];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ntn = N / BN;
-  const int ntiles = ((M + BM - 1) / BM) * ntn;
   const int nkt = K / 64;
   const int64_t row_bytes = (int64_t)K * 2;
-  int tm, tn;
-  tile_coords_of(blockIdx.x, ntn, ntiles, tm, tn);
   const int n0 = tn * BN;
 
   // this lane's bias columns: block j, columns 16 j + 4 (lane >> 4) + 0..3
@@ -203,6 +200,20 @@ __global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict_
       *reinterpret_cast<u32x4*>(C + (int64_t)row * N + n0 + q * 8) =
           *reinterpret_cast<const u32x4*>(ot + r * kOutRowBytes + q * 16);
   }
+}
+
+// A (M rows, K), Bt (N rows, K), C (M, N) bf16 bits; bias (N) fp32.
+__global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict__ A,
+                                                     const uint16_t* __restrict__ Bt,
+                                                     uint16_t* __restrict__ C,
+                                                     const float* __restrict__ bias, int M,
+                                                     int N, int K) {
+  __shared__ u32x4 smem[mid::NS * mid::kStage];
+  const int ntn = N / mid::BN;
+  const int ntiles = ((M + mid::BM - 1) / mid::BM) * ntn;
+  int tm, tn;
+  tile_coords_of(blockIdx.x, ntn, ntiles, tm, tn);
+  outproj_mid_tile(A, Bt, C, bias, M, N, K, tm, tn, smem);
 }
 
 }  // namespace dev

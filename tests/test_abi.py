@@ -362,12 +362,14 @@ def test_plan_flags(pkg, flags, ok):
 
 def test_forward_path_rules(pkg):
     """tmoe_forward_path's host-side selection (no GPU: as on a 256-compute-unit
-    MI355X): decode in one launch, the one-launch large-T forward, the wide-router
-    forward whose out-projection forms c (x) z itself, and the plain launches."""
+    MI355X): decode in one launch, the one-launch large-T and mid-T forwards, the
+    wide-router forward whose out-projection forms c (x) z itself, and the plain
+    launches."""
     cases = [("C2", 32, pkg._lib.TMOE_PATH_DECODE), ("C3", 16384, pkg._lib.TMOE_PATH_FUSED),
              ("C5", 16384, pkg._lib.TMOE_PATH_FUSED), ("C3", 4096, pkg._lib.TMOE_PATH_LARGE),
              ("C4", 4096, pkg._lib.TMOE_PATH_LARGE_KR), ("C4", 600, pkg._lib.TMOE_PATH_LARGE),
-             ("C3", 200, pkg._lib.TMOE_PATH_SMALL)]
+             ("C3", 2048, pkg._lib.TMOE_PATH_FUSED_MID), ("C3", 257, pkg._lib.TMOE_PATH_FUSED_MID),
+             ("C3", 3001, pkg._lib.TMOE_PATH_LARGE), ("C3", 200, pkg._lib.TMOE_PATH_SMALL)]
     for name, T, want in cases:
         w = pkg.WORKLOADS[name]
         m = pkg.TuckerMoE(w.d_in, w.d_out, w.cfg()).to(w.dtype)

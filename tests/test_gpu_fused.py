@@ -1,5 +1,6 @@
-"""The one-launch large-T forward (k_fused_large), the one-launch K-sliced mid-T
-front (k_front_sliced) and the reporting of lost in-launch signals.
+"""The one-launch large-T forward (k_fused_large), the one-launch mid-T forward
+(k_fused_mid), the one-launch K-sliced front (k_front_sliced) and the reporting of
+lost in-launch signals.
 
 The large-T forward of a folded bf16 plan (r3 = 256, E <= 32, d_out % 288 == 0,
 T >= 8192 at the C3 shapes) runs front and out-projection in one persistent grid
@@ -113,14 +114,18 @@ def test_fused_workspace_reuse_and_graph(pkg, dev):
 @pytest.mark.parametrize("T", [300, 777, 2048, 3001, 4096])
 def test_sliced_front_matches_two_launches(pkg, dev, T):
     """The K-sliced mid-T front in one launch (k_front_sliced: slices, then the
-    per-token epilogue once a tile's slices are in) against the same slices in two
-    launches (TMOE_FLAG_NO_FUSE: k_front_part + k_front_epi): bit-identical outputs
-    and routing, a clean status block, and the float64 oracle."""
+    per-token epilogue once a tile's slices are in; up to T = 2048 inside the
+    one-launch mid-T forward k_fused_mid, with the out-projection tiles) against the
+    same slices in separate launches (TMOE_FLAG_NO_FUSE: k_front_part + k_front_epi,
+    then the out-projection): bit-identical outputs and routing, a clean status
+    block, and the float64 oracle."""
     w = pkg.WORKLOADS["C3"]
     params = pkg.synth.make_params(w, affine="random")
     x = pkg.synth.make_x(w, T, stream=19)
     xd = x.to(dev)
     m = _module(pkg, dev, w, params)
+    want = pkg._lib.TMOE_PATH_FUSED_MID if T <= 2048 else pkg._lib.TMOE_PATH_LARGE
+    assert m.plan().forward_path(T) == want
     out, idx, wts = _forward(m, xd)
     m.check_signals()
     m2 = _module(pkg, dev, w, params, fuse=False)
@@ -135,10 +140,11 @@ def test_sliced_front_matches_two_launches(pkg, dev, T):
 
 
 def test_sliced_front_workspace_reuse_and_graph(pkg, dev):
-    """The one-launch sliced front does not depend on what the workspace held (0xFF
-    bytes, random bytes, the flags of the previous forward); a captured forward
-    (the two-launch sliced front) replays to the same bits, with eager forwards
-    between the replays."""
+    """The one-launch mid-T forward (k_fused_mid at T = 2048) does not depend on
+    what the workspace held (0xFF bytes, random bytes, the flags of the previous
+    forward); a captured forward (the sliced front in two launches, then the
+    out-projection) replays to the same bits, with eager forwards between the
+    replays."""
     w = pkg.WORKLOADS["C3"]
     T = 2048
     params = pkg.synth.make_params(w, affine="random")
@@ -181,7 +187,7 @@ def test_sliced_front_workspace_reuse_and_graph(pkg, dev):
 
 
 # workloads whose forward signals between work-groups of one launch: the
-# one-launch large-T forward (C3), the one-launch sliced front (C3 at T = 2048),
+# one-launch large-T forward (C3), the one-launch mid-T forward (C3 at T = 2048),
 # the E = 256 front (C4) and the decode launch (C2)
 @pytest.mark.parametrize("name,T", [("C3", 16384), ("C3", 2048), ("C4", 600), ("C2", 32)])
 def test_lost_signal_is_reported(pkg, dev, name, T):
