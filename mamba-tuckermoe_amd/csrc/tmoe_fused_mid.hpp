@@ -16,8 +16,9 @@
 //    slices, the epilogue of 64 / S of the tile's tokens, whose c (x) z rows it
 //    stores with plain stores), then sets its epilogue flag;
 //  * phase 2: waves 4-7 end; waves 0-3 take the XCD's out-projection tile i (row tile
-//    x + 8 (i / ntn), column tile i % ntn), wait for the 2 S epilogue flags of its row
-//    tile's front tiles and run k_outproj_mid's tile (outproj_mid_tile).
+//    x + 8 (i / ntn), column tile i % ntn), issue the DMAs of its first W^T tiles,
+//    wait for the 2 S epilogue flags of its row tile's front tiles and run
+//    k_outproj_mid's tile (outproj_mid_tile).
 // Same slices, same arithmetic as k_front_sliced + k_outproj_mid: bit-identical.
 //
 // Every work-group finishes phase 1 before it waits in phase 2, and all work-groups
@@ -50,7 +51,8 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fuse
   typedef FrontPartGeom<Elt, R3, NR, PFA, BM, NS, WMF> G;
   static_assert(BM * fmid::kFrontPerRow == mid::BM, "two front tiles per row tile");
   static_assert(64 * G::NWT >= 256, "the out-projection's four waves");
-  constexpr int kSlots = cmax(G::kSmemBytes / 16, mid::NS * mid::kStage);
+  // the out-projection's stages and one more slot for phase 2's wait
+  constexpr int kSlots = cmax(G::kSmemBytes / 16, mid::NS * mid::kStage + 1);
   __shared__ u32x4 smem[kSlots];
   const int x = xcc_id(), i = (int)blockIdx.x / fmid::kXcds;
   const int n_ft = (int)((a.T + BM - 1) / BM);
@@ -76,11 +78,15 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fuse
   const int rt = x + fmid::kXcds * (i / ntn), tn = i % ntn;
   const int f0 = fmid::kFrontPerRow * rt;
   const int nf = n_ft - f0 < fmid::kFrontPerRow ? n_ft - f0 : fmid::kFrontPerRow;
-  int* seen_all = reinterpret_cast<int*>(smem);
-  // on a lost signal (reported) the tile is computed from whatever the rows hold
-  (void)sync_await(a.sync + sync_flag((int64_t)(n_ft + f0) * S), nf * S, a.epoch, a.sync,
-                   seen_all, false, a.wait_polls, a.status);
-  outproj_mid_tile(A, Wt, C, bias, (int)a.T, N, K, rt, tn, smem);
+  // the wait's word of LDS: the slot past the NS stages (the DMAs issued before the
+  // wait write into the stages)
+  int* seen_all = reinterpret_cast<int*>(smem + mid::NS * mid::kStage);
+  // the tile's W^T DMAs go out before the wait; on a lost signal (reported) the tile
+  // is computed from whatever the rows hold
+  outproj_mid_tile(A, Wt, C, bias, (int)a.T, N, K, rt, tn, smem, [&] {
+    (void)sync_await(a.sync + sync_flag((int64_t)(n_ft + f0) * S), nf * S, a.epoch, a.sync,
+                     seen_all, false, a.wait_polls, a.status);
+  });
 }
 
 }  // namespace dev

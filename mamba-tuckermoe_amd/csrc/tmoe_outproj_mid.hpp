@@ -78,11 +78,15 @@ __device__ __forceinline__ void mid_step(f32x4m (&acc)[mid::FM][mid::FN],
 // Output tile (tm, tn) of out = A Bt^T + bias, by the work-group's threads 0 ..
 // 255 (waves 0-3; no other wave may be alive at its barriers). A (M rows, K), Bt
 // (N rows, K), C (M, N) bf16 bits; bias (N) fp32; smem: NS kStage 16-byte slots.
+// before(): runs after the first tiles' W^T DMAs are issued and before any read of
+// A (the one-launch forward's wait for its A rows).
+template <class Before>
 __device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
                                                  const uint16_t* __restrict__ Bt,
                                                  uint16_t* __restrict__ C,
                                                  const float* __restrict__ bias, int M, int N,
-                                                 int K, int tm, int tn, u32x4* smem) {
+                                                 int K, int tm, int tn, u32x4* smem,
+                                                 Before&& before) {
   using namespace mid;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -126,16 +130,26 @@ __device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
     else bf[b - FM] = s[lds_slot(BM + (b - FM) * 16 + (lane & 15), ch)];
   };
 
-  // prologue: tiles 0 .. NS - 2 in flight (those that exist), tile 0 landed, its
-  // first K step's fragments read
+  // prologue: tiles 0 .. NS - 2 in flight (those that exist), W^T blocks first (DMA
+  // instructions d >= kADma of each wave), then before(), then the A blocks; tile 0
+  // landed, its first K step's fragments read
+  constexpr int kADma = kABlocks / 4;   // a wave's A DMAs per tile: d < kADma
+  static_assert(kABlocks % 4 == 0, "a wave's A blocks are its first DMAs of a tile");
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
     if (t < nkt)
 #pragma unroll
-      for (int d = 0; d < kDmaPerWave; ++d) dma_one(t, t, d);
+      for (int d = kADma; d < kDmaPerWave; ++d) dma_one(t, t, d);
+  before();
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < nkt)
+#pragma unroll
+      for (int d = 0; d < kADma; ++d) dma_one(t, t, d);
   static_assert(NS == 4, "the waits below count the tiles issued after the one awaited");
-  if (nkt > 2) wait_vm_lds<2 * kDmaPerWave>();
-  else if (nkt > 1) wait_vm_lds<kDmaPerWave>();
+  // issued: the W^T blocks of tiles 0-2, then their A blocks
+  if (nkt > 2) wait_vm_lds<2 * kADma>();
+  else if (nkt > 1) wait_vm_lds<kADma>();
   else wait_vm_lds<0>();
   lds_barrier();
 #pragma unroll
@@ -160,9 +174,13 @@ __device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
     else mid_step<false>(acc, fa[0], fb[0], ld1);
     // tile kt + 1 has landed once at most the DMAs issued after it remain:
     // those of iteration kt - 1 (tile kt + 2 or a repeat; in iteration 0 the
-    // prologue's tile 2, if there is one)
-    if (kt == 0 && nkt <= 2) wait_vm_lds<0>();
-    else wait_vm_lds<kDmaPerWave>();
+    // prologue's A blocks of tile 2, if there is one)
+    if (kt == 0) {
+      if (nkt > 2) wait_vm_lds<kADma>();
+      else wait_vm_lds<0>();
+    } else {
+      wait_vm_lds<kDmaPerWave>();
+    }
     lds_barrier();
     const u32x4* sn = smem + ((kt + 1) % NS) * kStage;
     const int kd = cmin_dev(kt + NS - 1, nkt - 1), sd = (kt + NS - 1) % NS;
@@ -213,7 +231,7 @@ __global__ __launch_bounds__(256) void k_outproj_mid(const uint16_t* __restrict_
   const int ntiles = ((M + mid::BM - 1) / mid::BM) * ntn;
   int tm, tn;
   tile_coords_of(blockIdx.x, ntn, ntiles, tm, tn);
-  outproj_mid_tile(A, Bt, C, bias, M, N, K, tm, tn, smem);
+  outproj_mid_tile(A, Bt, C, bias, M, N, K, tm, tn, smem, [] {});
 }
 
 }  // namespace dev
