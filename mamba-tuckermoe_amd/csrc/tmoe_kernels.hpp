@@ -1240,8 +1240,19 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
   float* ue = rec_all + BM;
   const int mode = a.router_mode;
   const bool ue_lds = E * R1 * 4 <= ue_bytes;
-  if (ue_lds)
-    for (int i = threadIdx.x; i < E * R1; i += NT) ue[i] = a.uexp[i];
+  if (ue_lds) {
+    // four loads in flight per thread before their stores (a load-store loop waited
+    // for each load in turn)
+    constexpr int U = 4;
+    for (int i0 = threadIdx.x; i0 < E * R1; i0 += U * NT) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = i0 + u * NT < E * R1 ? a.uexp[i0 + u * NT] : 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (i0 + u * NT < E * R1) ue[i0 + u * NT] = v[u];
+    }
+  }
   const float* uex = ue_lds ? ue : a.uexp;
   const int gl = lane % G;
   for (int row0 = wave * RPW; row0 < BM; row0 += NWT * RPW) {
@@ -1252,14 +1263,20 @@ __device__ __forceinline__ void front_topk(const FwdArgs& a, int64_t m0, int row
     const int64_t g = m0 + row;
     uint64_t key[PL];   // 0 for columns past E
     float sv[PL];       // the scores the keys rank (router_mode 1: capped ones)
+    // every logit read before any is stored (a store behind a branch between the
+    // reads made each read wait for the one before)
 #pragma unroll
     for (int p = 0; p < PL; ++p) {
       const int col = gl + G * p;
       float sc = 0.f;
 #pragma unroll
       for (int w = 0; w < NP; ++w) sc += lg[(w * BM + row) * LD + col];
-      if (a.logits && live && col < E) a.logits[g * E + col] = sc;
       sv[p] = sc;
+    }
+    if (a.logits && live) {
+#pragma unroll
+      for (int p = 0; p < PL; ++p)
+        if (gl + G * p < E) a.logits[g * E + gl + G * p] = sv[p];
     }
     // a branch on the uniform mode: selected per key, the capped score's exp and
     // divisions ran for every key in mode 0 as well
