@@ -16,7 +16,7 @@
 //    slices, the epilogue of 64 / S of the tile's tokens, whose c (x) z rows it
 //    stores with plain stores), then sets its epilogue flag;
 //  * phase 2: waves 4-7 end; waves 0-3 take the XCD's out-projection tile i (row tile
-//    x + 8 (i / ntn), column tile i % ntn), issue the DMAs of its first W^T tiles,
+//    x + 8 (i / ntn), column tile i % ntn), issue the DMAs of its first W^T tile,
 //    wait for the 2 S epilogue flags of its row tile's front tiles and run
 //    k_outproj_mid's tile (outproj_mid_tile).
 // Same slices, same arithmetic as k_front_sliced + k_outproj_mid: bit-identical.
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fuse
   // the wait's word of LDS: the slot past the NS stages (the DMAs issued before the
   // wait write into the stages)
   int* seen_all = reinterpret_cast<int*>(smem + mid::NS * mid::kStage);
-  // the tile's W^T DMAs go out before the wait; on a lost signal (reported) the tile
+  // the first K tile's W^T DMAs go out before the wait; on a lost signal (reported) the tile
   // is computed from whatever the rows hold
   outproj_mid_tile(A, Wt, C, bias, (int)a.T, N, K, rt, tn, smem, [&] {
     (void)sync_await(a.sync + sync_flag((int64_t)(n_ft + f0) * S), nf * S, a.epoch, a.sync,

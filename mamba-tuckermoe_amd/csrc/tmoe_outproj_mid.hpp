@@ -78,7 +78,7 @@ __device__ __forceinline__ void mid_step(f32x4m (&acc)[mid::FM][mid::FN],
 // Output tile (tm, tn) of out = A Bt^T + bias, by the work-group's threads 0 ..
 // 255 (waves 0-3; no other wave may be alive at its barriers). A (M rows, K), Bt
 // (N rows, K), C (M, N) bf16 bits; bias (N) fp32; smem: NS kStage 16-byte slots.
-// before(): runs after the first tiles' W^T DMAs are issued and before any read of
+// before(): runs after the first tile's W^T DMAs are issued and before any read of
 // A (the one-launch forward's wait for its A rows).
 template <class Before>
 __device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
@@ -130,26 +130,28 @@ __device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
     else bf[b - FM] = s[lds_slot(BM + (b - FM) * 16 + (lane & 15), ch)];
   };
 
-  // prologue: tiles 0 .. NS - 2 in flight (those that exist), W^T blocks first (DMA
-  // instructions d >= kADma of each wave), then before(), then the A blocks; tile 0
-  // landed, its first K step's fragments read
+  // prologue: tiles 0 .. NS - 2 in flight (those that exist): tile 0's W^T blocks
+  // (DMA instructions d >= kADma of each wave), before(), tile 0's A blocks, then
+  // tiles 1 and 2 whole; tile 0 landed, its first K step's fragments read. Only one
+  // tile's W^T goes out before before(): a wait's first poll returns after every
+  // DMA issued ahead of it (the in-order vmcnt), and three tiles' W^T (55 KB) put
+  // ~1 us in front of the one-launch forward's poll (0.5 us per launch slower at
+  // T = 2048 than this order, same output).
   constexpr int kADma = kABlocks / 4;   // a wave's A DMAs per tile: d < kADma
   static_assert(kABlocks % 4 == 0, "a wave's A blocks are its first DMAs of a tile");
 #pragma unroll
-  for (int t = 0; t < NS - 1; ++t)
-    if (t < nkt)
-#pragma unroll
-      for (int d = kADma; d < kDmaPerWave; ++d) dma_one(t, t, d);
+  for (int d = kADma; d < kDmaPerWave; ++d) dma_one(0, 0, d);
   before();
 #pragma unroll
-  for (int t = 0; t < NS - 1; ++t)
+  for (int d = 0; d < kADma; ++d) dma_one(0, 0, d);
+#pragma unroll
+  for (int t = 1; t < NS - 1; ++t)
     if (t < nkt)
 #pragma unroll
-      for (int d = 0; d < kADma; ++d) dma_one(t, t, d);
+      for (int d = 0; d < kDmaPerWave; ++d) dma_one(t, t, d);
   static_assert(NS == 4, "the waits below count the tiles issued after the one awaited");
-  // issued: the W^T blocks of tiles 0-2, then their A blocks
-  if (nkt > 2) wait_vm_lds<2 * kADma>();
-  else if (nkt > 1) wait_vm_lds<kADma>();
+  if (nkt > 2) wait_vm_lds<2 * kDmaPerWave>();
+  else if (nkt > 1) wait_vm_lds<kDmaPerWave>();
   else wait_vm_lds<0>();
   lds_barrier();
 #pragma unroll
@@ -174,9 +176,9 @@ __device__ __forceinline__ void outproj_mid_tile(const uint16_t* __restrict__ A,
     else mid_step<false>(acc, fa[0], fb[0], ld1);
     // tile kt + 1 has landed once at most the DMAs issued after it remain:
     // those of iteration kt - 1 (tile kt + 2 or a repeat; in iteration 0 the
-    // prologue's A blocks of tile 2, if there is one)
+    // prologue's tile 2, if there is one)
     if (kt == 0) {
-      if (nkt > 2) wait_vm_lds<kADma>();
+      if (nkt > 2) wait_vm_lds<kDmaPerWave>();
       else wait_vm_lds<0>();
     } else {
       wait_vm_lds<kDmaPerWave>();
