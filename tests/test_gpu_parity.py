@@ -136,6 +136,18 @@ def test_mid_outproj_narrow(pkg, dev, fold):
     _check(w, got, onp.forward_f64(x, params, w.k), f"mid narrow/fold={fold}")
 
 
+@pytest.mark.parametrize("r2", [64, 128])
+def test_mid_outproj_short_k(pkg, dev, r2):
+    # the unfolded out-projection's K = r2: at 128, k_outproj_mid with two K tiles of
+    # 64 (its prologue's short case: every tile in flight before the first wait); at
+    # 64 the plan's core is k_core and its out-projection k_outproj_pp
+    w = pkg.Workload("custom", 1000, 256, 288, 8, 2, 2, 128, r2, torch.bfloat16, 81)
+    params = pkg.synth.make_params(w, affine="random")
+    x = pkg.synth.make_x(w)
+    got = _run(_module(pkg, dev, w, params, False), x, dev)
+    _check(w, got, onp.forward_f64(x, params, w.k), f"mid short K={r2}")
+
+
 @pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
 def test_wide_outproj_narrow(pkg, dev, fold):
     # (E, k, r1, r3, r2, d_in, d_out): K = 256 either way, 2 column tiles of 288
