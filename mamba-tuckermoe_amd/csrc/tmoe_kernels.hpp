@@ -1429,13 +1429,19 @@ __global__ __launch_bounds__(64 * WMF * (R3 / 32 < 4 ? R3 / 32 : 4)) void k_fron
 // share of x [U_in | W_r^T] with k_front's main loop and writes it as fp32 to raw
 // plane `slice` (T rows of r3 + E floats); k_front_epi then adds the planes in
 // plane order and runs the per-token epilogue (RMSNorm, top-k, softmax, c).
+// Both operands go to LDS by DMA, issued by every wave (a slice is 3-8 K tiles: the
+// whole slice is in flight after the first tiles' issue). With x through four
+// waves' register ring and the weights by the other four waves' DMA (k_front's
+// scheme) the slices took longer, bit-identical: at the C3 shapes k_front_sliced
+// 23.4 -> 20.8 us at T = 4096 and 21.3 -> 19.5 us at T = 3001, k_front_part 12.0 ->
+// 11.1 us and the one-launch k_fused_mid 30.6 -> 29.3 us at T = 2048.
 template <class Elt, int R3, int NR, int PFA = kFrontPFA, int BM = kFrontBM, int NS = 2,
           int WMF = kFrontWM>
 struct FrontPartGeom {
   static constexpr int EP = 32 * NR;
   static constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;
   static constexpr int NWT = NW * WMF;
-  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
+  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, true, true, 0> TL;
   typedef RouterExtra<Elt, TL::FM, NR, NW> RX;
   static constexpr int LD = EP + 1;
   static constexpr int kPlanes = RX::kSplitK ? NW : 1;
