@@ -19,7 +19,9 @@ constexpr size_t kStaticScratchBytes = (size_t)48 << 20;
 hipError_t static_scratch(hipStream_t stream, void** ptr);
 
 constexpr int kFrontBM = 64;    // tokens per k_front work-group (whole r3 and E rows)
-constexpr int kFrontPFA = 8;    // K tiles of x in flight per k_front work-group
+// depth of an x register ring (Tile's PFA); the fronts' loops now bring x to LDS
+// by DMA, where the ring depth has no effect
+constexpr int kFrontPFA = 8;
 constexpr int kFrontWM = 2;     // row groups of waves per k_front work-group
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 256;

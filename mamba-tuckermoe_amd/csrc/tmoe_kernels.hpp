@@ -1350,10 +1350,12 @@ __device__ __forceinline__ void front_tile(const FwdArgs& a, int tile) {
   constexpr int EP = 32 * NR;
   constexpr int NW = R3 / 32 < 4 ? R3 / 32 : 4;   // waves across the z columns
   constexpr int NWT = NW * WMF;                      // all waves (WMF row groups)
-  // x streams from HBM once: a register ring of PFA K tiles, run by half of the
-  // waves. The weight rows come from L2 by DMA into LDS (the other half), shared
-  // by the WMF row groups.
-  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, false, true, NWT / 2> TL;
+  // x (streamed from HBM once) and the weight rows (from L2, shared by the WMF row
+  // groups) both go to LDS by DMA from every wave. With x through half of the
+  // waves' register ring (PFA K tiles ahead) and the weights by the other half's
+  // DMA the launch took longer, bit-identical: 26.6-26.7 against 24.4-25.0 us at
+  // the C3 shapes, T = 6144 (32-token tiles).
+  typedef Tile<BM, R3, EP, WMF, NW, PFA, 1, NS, true, true, 0> TL;
   constexpr int FM = TL::FM;   // a wave covers the BM / WMF rows of its group
   typedef RouterExtra<Elt, FM, NR, NW> RX;
   // epilogue LDS: staged z tile, then the logits plane(s), then RMSNorm partials
@@ -1553,8 +1555,11 @@ __global__ __launch_bounds__(256) void k_front_split(FwdArgs a) {
   typedef typename Elt::T T;
   constexpr int BM = 32, EP = 32 * NR, NW = 4;
   static_assert(R3 == 256 && EP >= 128, "split front: r3 = 256, E_pad >= 128");
-  typedef Tile<BM, R3, 0, 1, NW, PFA, 1, NS, false, true, NW / 2> TLZ;
-  typedef Tile<BM, EP, 0, 1, NW, PFA, 1, NS, false, true, NW / 2> TLR;
+  // x and the weight rows both by LDS DMA from every wave (with x through two waves'
+  // register ring and the weights by the other two's DMA the launch took 26.9-27.1
+  // against 22.8-22.9 us at C4, bit-identical)
+  typedef Tile<BM, R3, 0, 1, NW, PFA, 1, NS, true, true, 0> TLZ;
+  typedef Tile<BM, EP, 0, 1, NW, PFA, 1, NS, true, true, 0> TLR;
   constexpr int LD = EP + 1;
   constexpr int kZEpi = TileStage<TLZ, T>::kBytes + (NW * BM + BM) * 4;
   constexpr int kREpi = (BM * LD + kTopkRecFloats<BM>) * 4;
