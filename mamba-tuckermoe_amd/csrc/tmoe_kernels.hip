@@ -97,7 +97,8 @@ hipError_t launch_front_nr(const FwdArgs& a, hipStream_t st) {
   }
   if constexpr (R3 == 256 && NR == 1 && std::is_same<Elt, EltBF16>::value) {
     // the weight operand from registers (k_front_ks): 64-token tiles, 8 waves
-    // (measured at T = 16384: 31.7 against 33.7 us for k_front)
+    // (measured at T = 16384: 31.7 against 33.7 us for k_front; with k_front's x
+    // by DMA, 39.6-40.0 against 40.5-40.7 us in the bench's rotated-input loop)
     if (a.wfrag) {
       hipLaunchKernelGGL((dev::k_front_ks<R3, NR>), dim3(cdiv(a.T, 64)), dim3(512), 0, st, a,
                          static_cast<const uint16_t*>(a.wfrag));
